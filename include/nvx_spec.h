@@ -1,0 +1,182 @@
+/*
+ * nvx_spec.h -- C ABI of libnvx_spec.so, the MI355X (gfx950) speculative-decoding
+ * verify path: n-gram drafter, paged tree attention, temperature softmax + tree /
+ * chain rejection sampling, KV-cache slot scatter and accepted-path compaction.
+ *
+ * Conventions
+ *   - Plain pointers to device memory, sizes in elements unless a name says
+ *     _bytes.  The caller owns every buffer; no entry point allocates device
+ *     memory.  Work is enqueued on `stream` (a hipStream_t; NULL = legacy
+ *     default stream) and never synchronises the host.
+ *   - Return 0 on success, a negative NVX_E* code otherwise; nvx_last_error()
+ *     returns a message for the calling thread's last failure.
+ *   - The reference (nano-vllm 0.2.0) exposes these as Python modules, not a C
+ *     ABI; each declaration cites the reference interface it replaces or feeds.
+ *     The Python host mirror (nano-vllm-x_amd/nanovllm) binds them with ctypes.
+ */
+#ifndef NVX_SPEC_H
+#define NVX_SPEC_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NVX_OK 0
+#define NVX_EINVAL -1 /* bad argument (shape, dtype, alignment, range) */
+#define NVX_EHIP -2   /* HIP runtime error (launch, event) */
+
+#define NVX_DTYPE_F32 0
+#define NVX_DTYPE_BF16 1
+#define NVX_DTYPE_F16 2
+
+/* Library version (major*10000 + minor*100 + patch). */
+int nvx_version(void);
+
+/* Message for the calling thread's most recent failure ("" if none). */
+const char* nvx_last_error(void);
+
+/* ------------------------------------------------------------------ drafter --
+ * N-gram prompt-lookup drafting over a packed batch of token histories.
+ * Feeds from Sequence.token_ids (reference nanovllm/engine/sequence.py:21,
+ * :67-70); the reference has no drafter.  Semantics of transformers'
+ * PromptLookupCandidateGenerator.get_candidates: for n = min(max_ngram, L-1)
+ * down to min_ngram, the left-most earlier occurrence of the last n tokens whose
+ * continuation is non-empty wins; propose up to num_draft following tokens.
+ *   tokens  int32 [offsets[num_seqs]]     offsets int64 [num_seqs + 1]
+ *   draft   int32 [num_seqs, num_draft]   (-1 padded)   draft_len int32 [num_seqs]
+ * Limits: 1 <= min_ngram <= max_ngram <= 8, num_draft >= 1.
+ */
+int nvx_ngram_propose(const int32_t* tokens, const int64_t* offsets, int32_t num_seqs,
+                      int32_t min_ngram, int32_t max_ngram, int32_t num_draft,
+                      int32_t* draft, int32_t* draft_len, void* stream);
+
+/* ------------------------------------------------------------ KV slot scatter --
+ * Replaces store_kvcache / store_kvcache_kernel (reference
+ * nanovllm/layers/attention.py:10-40): for i < num_tokens with
+ * slot_mapping[i] != -1, copy row_bytes bytes from key + i*key_stride_bytes to
+ * k_cache + slot*row_bytes, and likewise value -> v_cache.
+ */
+int nvx_store_kvcache(const void* key, int64_t key_stride_bytes, const void* value,
+                      int64_t value_stride_bytes, void* k_cache, void* v_cache,
+                      const int32_t* slot_mapping, int32_t num_tokens, int32_t row_bytes,
+                      void* stream);
+
+/* ------------------------------------------------------------- KV compaction --
+ * Moves the accepted path of each verified draft tree into contiguous cache
+ * positions, for num_layers layers of K and V: row(ctx + d) <- row(ctx + path[d])
+ * for d = 1..accepted_len[b], where row(pos) is slot
+ * block_tables[b][pos / block_size] * block_size + pos % block_size (reference slot
+ * formula, nanovllm/engine/model_runner.py:151-161, :181; cache layout :115).
+ * Generalises store_kvcache (attention.py:21-30) to a cache-resident source; the
+ * reference has no compaction.  Layer l of K lives at k_cache + l*layer_stride_bytes.
+ *   block_tables int32 [num_seqs, block_table_stride]   ctx_lens int32 [num_seqs]
+ *   path int32 [num_seqs, path_stride]                    accepted_len int32 [num_seqs]
+ */
+int nvx_kv_compact(void* k_cache, void* v_cache, int64_t layer_stride_bytes,
+                   int32_t num_layers, int32_t row_bytes, int32_t block_size,
+                   const int32_t* block_tables, int32_t block_table_stride,
+                   const int32_t* ctx_lens, const int32_t* path, int32_t path_stride,
+                   const int32_t* accepted_len, int32_t num_seqs, void* stream);
+
+/* ----------------------------------------------------------- tree attention --
+ * Paged attention of q_len query rows per sequence against the paged KV cache,
+ * with an ancestor mask over the sequence's last q_len cached positions.  Replaces
+ * the decode call flash_attn_with_kvcache(..., cache_seqlens=context_lens,
+ * block_table=block_tables, softmax_scale=scale, causal=True) (reference
+ * nanovllm/layers/attention.py:71-74) and, with tree_mask = NULL, the prefill call
+ * flash_attn_varlen_func(..., causal=True, block_table=...) (:64-70) once the
+ * prompt's K/V are in the cache.
+ *   q, o          bf16 [cu_seqlens_q[num_seqs], num_heads, 128]
+ *   k/v_cache     bf16 [*, block_size, num_kv_heads, 128]   (model_runner.py:115)
+ *   block_tables  int32 [num_seqs, block_table_stride]
+ *   cu_seqlens_q  int32 [num_seqs + 1]      context_lens int32 [num_seqs] (includes q rows)
+ *   tree_mask     uint64 [total q rows] or NULL: bit m of row i's mask makes key
+ *                 (context_len - q_len + m) visible; NULL = causal (m <= i).
+ *                 With a mask, q_len <= 64.
+ *   workspace     device scratch of nvx_tree_attention_workspace_size() bytes
+ *                 (may be NULL when that size is 0).
+ * Limits: head_dim == 128, block_size % 64 == 0, num_heads % num_kv_heads == 0.
+ */
+size_t nvx_tree_attention_workspace_size(int32_t num_seqs, int32_t total_q, int32_t max_seqlen_q,
+                                         int32_t max_context_len, int32_t num_heads,
+                                         int32_t num_kv_heads, int32_t head_dim);
+
+int nvx_tree_attention(const void* q, void* o, const void* k_cache, const void* v_cache,
+                       const int32_t* block_tables, int32_t block_table_stride,
+                       const int32_t* cu_seqlens_q, const int32_t* context_lens,
+                       const uint64_t* tree_mask, int32_t num_seqs, int32_t total_q,
+                       int32_t max_seqlen_q, int32_t max_context_len, int32_t num_heads,
+                       int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                       float scale, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------- temperature softmax --
+ * probs[r] = softmax(float(logits[r]) / temperatures[r]) in fp32 (reference
+ * nanovllm/layers/sampler.py:9-10).  Rows with temperature 0 are greedy: the fp32
+ * logits are written unchanged (only their argmax is used downstream).
+ *   logits  [num_rows, logits_row_stride] of logits_dtype (F32 or BF16)
+ *   probs   fp32 [num_rows, vocab] (contiguous)
+ */
+int nvx_temperature_softmax(const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
+                            const float* temperatures, float* probs, int32_t num_rows,
+                            int32_t vocab, void* stream);
+
+/* -------------------------------------------------- tree rejection sampling --
+ * Verifies one draft tree per sequence and emits the accepted path plus one
+ * recovered/bonus token.  Sits beside Sampler.forward (reference
+ * nanovllm/layers/sampler.py:5-12), whose categorical draw it generalises; the
+ * reference has no rejection sampler.  Node 0 is the root (the last committed
+ * token); parents[b][0] = -1 and parents[b][i] < i.  From the root, the children
+ * of the current node are tested in ascending node order:
+ *   accept child c (token x) iff  U[c] * q[x] <= cur[x]  and  cur[x] > 0,
+ *   q = draft row of the current node (draft_mode 0) or a point mass on x
+ *   (draft_mode 1); a rejection replaces cur by norm(max(cur - q, 0)).
+ * When no child is accepted (or the node is a leaf) the next token is drawn from
+ * cur by inverse CDF with final_uniforms[b].  Greedy rows (greedy[b] != 0): accept
+ * the first child whose token is the row argmax; else next = argmax.
+ *   target_probs  fp32, row (b, i) at  b*p_seq_stride + i*vocab   (rows are vocab long)
+ *   draft_probs   fp32, row (b, i) at  b*q_seq_stride + i*vocab   (NULL in draft_mode 1)
+ *   tokens, parents int32 [num_seqs, node_stride]; num_nodes int32 [num_seqs] or NULL
+ *   uniforms fp32 [num_seqs, node_stride] in [0,1); final_uniforms fp32 [num_seqs]
+ *   greedy uint8 [num_seqs] or NULL (all sampled)
+ * Outputs: path int32 [num_seqs, node_stride] (accepted node ids from the root,
+ * -1 padded), accepted_len int32 [num_seqs] (accepted draft nodes), out_tokens
+ * int32 [num_seqs, node_stride] (accepted tokens then the next token, -1 padded),
+ * next_token int32 [num_seqs].  Limits: 1 <= node_stride <= 64.
+ */
+int nvx_rejection_sample_tree(const float* target_probs, int64_t p_seq_stride,
+                              const float* draft_probs, int64_t q_seq_stride, int32_t vocab,
+                              const int32_t* tokens, const int32_t* parents,
+                              const int32_t* num_nodes, int32_t node_stride,
+                              const float* uniforms, const float* final_uniforms,
+                              const uint8_t* greedy, int32_t draft_mode, int32_t num_seqs,
+                              int32_t* path, int32_t* accepted_len, int32_t* out_tokens,
+                              int32_t* next_token, void* stream);
+
+/* ------------------------------------------------------------------ timing --
+ * Optional per-entry-point HIP-event timing on the launch stream (used by the
+ * benchmark to measure kernel durations in its timed region).
+ * kernel ids: 0 ngram, 1 store_kvcache, 2 kv_compact, 3 tree_attention,
+ *             4 temperature_softmax, 5 rejection_sample_tree.
+ */
+#define NVX_TIMER_NGRAM 0
+#define NVX_TIMER_STORE_KV 1
+#define NVX_TIMER_KV_COMPACT 2
+#define NVX_TIMER_TREE_ATTENTION 3
+#define NVX_TIMER_SOFTMAX 4
+#define NVX_TIMER_REJECTION 5
+#define NVX_TIMER_COUNT 6
+
+int nvx_timing_enable(int on);
+/* Synchronises the recorded events and returns the accumulated milliseconds and
+ * launch count for one kernel id since the last reset. */
+int nvx_timing_read(int32_t kernel_id, double* total_ms, int64_t* count);
+int nvx_timing_reset(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NVX_SPEC_H */

@@ -1,0 +1,406 @@
+// Paged tree attention for gfx950 (bf16 in, fp32 accumulate, bf16 out).
+//
+// Work item = (sequence b, KV head hk, q-row chunk, KV split).  The q rows of a
+// work item are the G = Hq/Hkv query heads of hk times the sequence's q_len tree
+// nodes (row r -> node r / G, head hk*G + r % G), so one staged K/V chunk serves
+// the whole GQA group.  Each wave owns 32 q rows.
+//
+// Per 64-key chunk the workgroup stages K (row-major) and V (transposed) in LDS,
+// then every wave computes S^T = K . Q^T with v_mfma_f32_32x32x16_bf16: lane l then
+// holds query row l%32 and 16 keys per 32-key tile, so the online-softmax row max
+// and row sum are in-lane plus one exchange with lane l^32.  P^T goes straight from
+// those registers into the B operand of O^T += V^T . P^T (the contraction slots are
+// relabelled to the keys the lane already holds; V^T is read with two 8-byte LDS
+// reads per MFMA).  Global loads of chunk c+1 are issued before computing chunk c.
+//
+// Masking: keys < context_len - q_len are visible to all rows; key base+m is
+// visible to node i iff bit m of its tree mask (or m <= i without a mask).
+// With more than one split, partial (o, log2-sum-exp) go to the workspace and a
+// second kernel merges them.
+#include "nvx_internal.h"
+
+namespace {
+
+constexpr int kD = 128;
+constexpr int kKC = 64;            // keys per staged chunk
+constexpr int kKStride = kD + 8;   // bf16 per K row in LDS (272 B: 16-B aligned, bank-skewed)
+constexpr int kVStride = kKC + 8;  // bf16 per V^T row in LDS (144 B)
+constexpr int kTargetWaves = 256 * 16;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+struct AttnParams {
+  const uint16_t* q;
+  uint16_t* o;
+  const uint16_t* k_cache;
+  const uint16_t* v_cache;
+  const int32_t* block_tables;
+  const int32_t* cu_q;
+  const int32_t* ctx_lens;
+  const uint64_t* tree_mask;
+  float* part_o;
+  float* part_lse;
+  int bt_stride, num_seqs, total_q, Hq, Hkv, G, block_size, nq, nsplit;
+  float scale_log2;
+};
+
+__device__ __forceinline__ uint16_t f2bf(float x) {
+  uint32_t u = __float_as_uint(x);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ int remap_xcd(int phys, int n) {
+  // Blocks are dispatched round-robin over the 8 XCDs; give each XCD a
+  // contiguous range of logical ids so the blocks of one (seq, kv head), which
+  // read the same K/V, share an L2.
+  const int x = phys & 7, slot = phys >> 3;
+  const int q = n >> 3, r = n & 7;
+  const int start = x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q;
+  return start + slot;
+}
+
+template <int W>
+__global__ __launch_bounds__(W * 64) void tree_attn_kernel(AttnParams p) {
+  constexpr int NT = W * 64;
+  constexpr int SEGS = (kKC * kD / 8) / NT;  // 16-byte K (and V) pieces per thread per chunk
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[kKC * kKStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kD * kVStride];
+
+  const int logical = remap_xcd(blockIdx.x, gridDim.x);
+  const int split = logical % p.nsplit;
+  int t = logical / p.nsplit;
+  const int qc = t % p.nq;
+  t /= p.nq;
+  const int hk = t % p.Hkv;
+  const int b = t / p.Hkv;
+
+  const int q0 = p.cu_q[b];
+  const int qlen = p.cu_q[b + 1] - q0;
+  const int ctxlen = p.ctx_lens[b];
+  const int base = ctxlen - qlen;
+  const int rows_total = p.G * qlen;
+  const int row0 = qc * W * 32;
+  if (row0 >= rows_total || qlen <= 0) return;  // uniform over the block
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, g = lane >> 5, lr = lane & 31;
+  const int r = row0 + wave * 32 + lr;
+  const bool row_ok = r < rows_total;
+  const int node = row_ok ? r / p.G : 0;
+  const int head = hk * p.G + (row_ok ? r % p.G : 0);
+  const int token = q0 + node;
+  const bool wave_active = row0 + wave * 32 < rows_total;
+
+  // Q^T fragments (B operand of S^T = K.Q^T): d = 16*s + 8*g + [0..7].
+  bf16x8 bq[8];
+  {
+    const uint16_t* qrow = p.q + ((int64_t)token * p.Hq + head) * kD + 8 * g;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (row_ok && token < p.total_q) v = *reinterpret_cast<const uint4*>(qrow + 16 * s);
+      bq[s] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
+  const uint64_t mbits = (p.tree_mask && row_ok && token < p.total_q) ? p.tree_mask[token] : 0ull;
+  const bool use_tree = p.tree_mask != nullptr;
+
+  // Keys beyond the last node of this chunk's rows are masked for every row.
+  const int last_node = min(qlen - 1, (row0 + W * 32 - 1) / p.G);
+  const int key_end = max(0, min(ctxlen, base + last_node + 1));
+  const int nchunks = (key_end + kKC - 1) / kKC;
+  const int cps = (nchunks + p.nsplit - 1) / p.nsplit;
+  const int c0 = split * cps;
+  const int c1 = min(nchunks, c0 + cps);
+
+  const int32_t* bt = p.block_tables + (int64_t)b * p.bt_stride;
+  const int bs = p.block_size;
+
+  uint4 kreg[SEGS], vreg[SEGS];
+  auto load_chunk = [&](int c) {
+#pragma unroll
+    for (int i = 0; i < SEGS; ++i) {
+      const int sid = tid + i * NT;
+      const int key = sid >> 4, seg = sid & 15;
+      const int pos = c * kKC + key;
+      kreg[i] = make_uint4(0, 0, 0, 0);
+      vreg[i] = make_uint4(0, 0, 0, 0);
+      if (pos < ctxlen && pos / bs < p.bt_stride) {
+        const int32_t blk = bt[pos / bs];
+        if (blk >= 0) {
+          const int64_t off = (((int64_t)blk * bs + pos % bs) * p.Hkv + hk) * kD + seg * 8;
+          kreg[i] = *reinterpret_cast<const uint4*>(p.k_cache + off);
+          vreg[i] = *reinterpret_cast<const uint4*>(p.v_cache + off);
+        }
+      }
+    }
+  };
+  auto store_chunk = [&]() {
+#pragma unroll
+    for (int i = 0; i < SEGS; ++i) {
+      const int sid = tid + i * NT;
+      const int key = sid >> 4, seg = sid & 15;
+      *reinterpret_cast<uint4*>(&k_lds[key * kKStride + seg * 8]) = kreg[i];
+      const uint32_t w[4] = {vreg[i].x, vreg[i].y, vreg[i].z, vreg[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        vt_lds[(seg * 8 + 2 * j) * kVStride + key] = (uint16_t)(w[j] & 0xffffu);
+        vt_lds[(seg * 8 + 2 * j + 1) * kVStride + key] = (uint16_t)(w[j] >> 16);
+      }
+    }
+  };
+
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x16 oacc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) oacc[dt][j] = 0.f;
+
+  if (c0 < c1) load_chunk(c0);
+  for (int c = c0; c < c1; ++c) {
+    __syncthreads();
+    store_chunk();
+    __syncthreads();
+    if (c + 1 < c1) load_chunk(c + 1);
+    if (!wave_active) continue;
+
+    // S^T tiles: keys kt*32 + (j/4)*8 + 4*g + j%4, query row lr.
+    f32x16 sacc[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) sacc[kt][j] = 0.f;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const bf16x8 a =
+            *reinterpret_cast<const bf16x8*>(&k_lds[(kt * 32 + lr) * kKStride + 16 * s + 8 * g]);
+        sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq[s], sacc[kt], 0, 0, 0);
+      }
+    }
+    const int pos0 = c * kKC;
+    const bool need_mask = pos0 + kKC > base;
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float sv = sacc[kt][j] * p.scale_log2;
+        if (need_mask) {
+          const int key = pos0 + kt * 32 + (j >> 2) * 8 + 4 * g + (j & 3);
+          bool vis = key < ctxlen;
+          if (vis && key >= base) {
+            const int mm = key - base;
+            vis = use_tree ? (((mbits >> mm) & 1ull) != 0ull) : (mm <= node);
+          }
+          if (!vis) sv = -INFINITY;
+        }
+        sacc[kt][j] = sv;
+        mloc = fmaxf(mloc, sv);
+      }
+    }
+    mloc = fmaxf(mloc, nvx::shfl_xor_f(mloc, 32));
+    const float m_new = fmaxf(m_run, mloc);
+    const bool dead = (m_new == -INFINITY);
+    const float alpha = dead ? 1.f : exp2f(m_run - m_new);
+    float lsum = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float pv = dead ? 0.f : exp2f(sacc[kt][j] - m_new);
+        sacc[kt][j] = pv;
+        lsum += pv;
+      }
+    lsum += nvx::shfl_xor_f(lsum, 32);
+    l_run = l_run * alpha + lsum;
+    m_run = m_new;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
+
+    // P^T as B operand: slot (g, i) of k-step ks holds key 16*ks + (i/4)*8 + 4*g + i%4.
+    bf16x8 bp[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) bp[ks][i] = (__bf16)sacc[ks >> 1][(ks & 1) * 8 + i];
+
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const uint16_t* vrow = &vt_lds[(dt * 32 + lr) * kVStride + 4 * g];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vrow + 16 * ks);
+        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vrow + 16 * ks + 8);
+        const bf16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bp[ks], oacc[dt], 0, 0, 0);
+      }
+    }
+  }
+
+  if (!row_ok || token >= p.total_q) return;
+  const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+  if (p.nsplit == 1) {
+    uint16_t* orow = p.o + ((int64_t)token * p.Hq + head) * kD;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int jg = 0; jg < 4; ++jg) {
+        const int d = dt * 32 + jg * 8 + 4 * g;
+        uint2 pk;
+        pk.x = (uint32_t)f2bf(oacc[dt][jg * 4 + 0] * inv) | ((uint32_t)f2bf(oacc[dt][jg * 4 + 1] * inv) << 16);
+        pk.y = (uint32_t)f2bf(oacc[dt][jg * 4 + 2] * inv) | ((uint32_t)f2bf(oacc[dt][jg * 4 + 3] * inv) << 16);
+        *reinterpret_cast<uint2*>(orow + d) = pk;
+      }
+  } else {
+    const int64_t prow = ((int64_t)split * p.total_q + token) * p.Hq + head;
+    float* po = p.part_o + prow * kD;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int jg = 0; jg < 4; ++jg) {
+        const int d = dt * 32 + jg * 8 + 4 * g;
+        *reinterpret_cast<float4*>(po + d) =
+            make_float4(oacc[dt][jg * 4 + 0] * inv, oacc[dt][jg * 4 + 1] * inv,
+                        oacc[dt][jg * 4 + 2] * inv, oacc[dt][jg * 4 + 3] * inv);
+      }
+    if (g == 0) p.part_lse[prow] = l_run > 0.f ? m_run + log2f(l_run) : -INFINITY;
+  }
+}
+
+// Merge split partials: o = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M).
+__global__ __launch_bounds__(kD) void combine_kernel(const float* __restrict__ part_o,
+                                                     const float* __restrict__ part_lse,
+                                                     uint16_t* __restrict__ o, int rows, int nsplit) {
+  const int row = blockIdx.x;  // token * Hq + head
+  const int d = threadIdx.x;
+  float M = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, part_lse[(int64_t)s * rows + row]);
+  float num = 0.f, den = 0.f;
+  if (M != -INFINITY) {
+    for (int s = 0; s < nsplit; ++s) {
+      const float lse = part_lse[(int64_t)s * rows + row];
+      if (lse == -INFINITY) continue;
+      const float w = exp2f(lse - M);
+      den += w;
+      num += w * part_o[((int64_t)s * rows + row) * kD + d];
+    }
+  }
+  o[(int64_t)row * kD + d] = f2bf(den > 0.f ? num / den : 0.f);
+}
+
+struct Plan {
+  int W, nq, nsplit;
+};
+
+Plan make_plan(int num_seqs, int max_q, int max_ctx, int Hq, int Hkv) {
+  const int G = Hq / Hkv;
+  const int rows = G * (max_q > 0 ? max_q : 1);
+  int W = 1;
+  while (W < 8 && W * 32 < rows) W *= 2;
+  Plan pl;
+  pl.W = W;
+  pl.nq = (rows + W * 32 - 1) / (W * 32);
+  const int64_t waves = (int64_t)num_seqs * Hkv * pl.nq * W;
+  int ns = (int)((kTargetWaves + waves - 1) / (waves > 0 ? waves : 1));
+  const int max_chunks = (max_ctx + kKC - 1) / kKC;
+  const int cap = max(1, max_chunks / 2);
+  if (ns > cap) ns = cap;
+  if (ns < 1) ns = 1;
+  pl.nsplit = ns;
+  return pl;
+}
+
+size_t workspace_bytes_for(const Plan& pl, int total_q, int Hq) {
+  if (pl.nsplit <= 1) return 0;
+  return (size_t)pl.nsplit * total_q * Hq * (kD + 1) * sizeof(float);
+}
+
+}  // namespace
+
+extern "C" size_t nvx_tree_attention_workspace_size(int32_t num_seqs, int32_t total_q,
+                                                    int32_t max_seqlen_q, int32_t max_context_len,
+                                                    int32_t num_heads, int32_t num_kv_heads,
+                                                    int32_t head_dim) {
+  if (num_seqs <= 0 || total_q <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
+      head_dim != kD)
+    return 0;
+  const Plan pl = make_plan(num_seqs, max_seqlen_q, max_context_len, num_heads, num_kv_heads);
+  return workspace_bytes_for(pl, total_q, num_heads);
+}
+
+extern "C" int nvx_tree_attention(const void* q, void* o, const void* k_cache, const void* v_cache,
+                                  const int32_t* block_tables, int32_t block_table_stride,
+                                  const int32_t* cu_seqlens_q, const int32_t* context_lens,
+                                  const uint64_t* tree_mask, int32_t num_seqs, int32_t total_q,
+                                  int32_t max_seqlen_q, int32_t max_context_len, int32_t num_heads,
+                                  int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                  float scale, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  nvx::clear_error();
+  NVX_CHECK(head_dim == kD, "tree_attention: head_dim must be %d (got %d)", kD, head_dim);
+  NVX_CHECK(num_kv_heads >= 1 && num_heads >= num_kv_heads && num_heads % num_kv_heads == 0,
+            "tree_attention: num_heads (%d) must be a multiple of num_kv_heads (%d)", num_heads,
+            num_kv_heads);
+  NVX_CHECK(block_size >= kKC && block_size % kKC == 0,
+            "tree_attention: block_size must be a positive multiple of %d (got %d)", kKC, block_size);
+  NVX_CHECK(num_seqs >= 0 && total_q >= 0 && max_seqlen_q >= 0 && max_context_len >= 0,
+            "tree_attention: negative size");
+  NVX_CHECK(tree_mask == nullptr || max_seqlen_q <= 64,
+            "tree_attention: a tree mask allows at most 64 query rows per sequence (got %d)",
+            max_seqlen_q);
+  NVX_CHECK(block_table_stride >= 1, "tree_attention: block_table_stride must be >= 1");
+  if (num_seqs == 0 || total_q == 0) return NVX_OK;
+  NVX_CHECK(q && o && k_cache && v_cache && block_tables && cu_seqlens_q && context_lens,
+            "tree_attention: null pointer");
+  const Plan pl = make_plan(num_seqs, max_seqlen_q, max_context_len, num_heads, num_kv_heads);
+  const size_t need = workspace_bytes_for(pl, total_q, num_heads);
+  NVX_CHECK(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+            "tree_attention: workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+
+  AttnParams p;
+  p.q = (const uint16_t*)q;
+  p.o = (uint16_t*)o;
+  p.k_cache = (const uint16_t*)k_cache;
+  p.v_cache = (const uint16_t*)v_cache;
+  p.block_tables = block_tables;
+  p.cu_q = cu_seqlens_q;
+  p.ctx_lens = context_lens;
+  p.tree_mask = tree_mask;
+  p.part_o = (float*)workspace;
+  p.part_lse = pl.nsplit > 1 ? (float*)workspace + (size_t)pl.nsplit * total_q * num_heads * kD : nullptr;
+  p.bt_stride = block_table_stride;
+  p.num_seqs = num_seqs;
+  p.total_q = total_q;
+  p.Hq = num_heads;
+  p.Hkv = num_kv_heads;
+  p.G = num_heads / num_kv_heads;
+  p.block_size = block_size;
+  p.nq = pl.nq;
+  p.nsplit = pl.nsplit;
+  p.scale_log2 = scale * 1.4426950408889634f;
+
+  hipStream_t s = (hipStream_t)stream;
+  nvx::TimerScope timer(NVX_TIMER_TREE_ATTENTION, s);
+  const int64_t nblocks = (int64_t)num_seqs * num_kv_heads * pl.nq * pl.nsplit;
+  NVX_CHECK(nblocks < (1ll << 31), "tree_attention: grid too large");
+  const dim3 grid((unsigned)nblocks);
+  switch (pl.W) {
+    case 1: hipLaunchKernelGGL(tree_attn_kernel<1>, grid, dim3(64), 0, s, p); break;
+    case 2: hipLaunchKernelGGL(tree_attn_kernel<2>, grid, dim3(128), 0, s, p); break;
+    case 4: hipLaunchKernelGGL(tree_attn_kernel<4>, grid, dim3(256), 0, s, p); break;
+    default: hipLaunchKernelGGL(tree_attn_kernel<8>, grid, dim3(512), 0, s, p); break;
+  }
+  NVX_LAUNCHED();
+  if (pl.nsplit > 1) {
+    hipLaunchKernelGGL(combine_kernel, dim3(total_q * num_heads), dim3(kD), 0, s, p.part_o,
+                       p.part_lse, (uint16_t*)o, total_q * num_heads, pl.nsplit);
+    NVX_LAUNCHED();
+  }
+  return NVX_OK;
+}

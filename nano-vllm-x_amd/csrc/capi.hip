@@ -1,0 +1,118 @@
+// Error reporting, version and the optional per-kernel HIP-event timers.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <mutex>
+#include <vector>
+
+#include "nvx_internal.h"
+
+namespace {
+thread_local char g_err[1024] = "";
+
+struct Pending {
+  int id;
+  hipEvent_t start, stop;
+};
+
+std::mutex g_mu;
+bool g_timing = false;
+std::vector<Pending> g_pending;
+std::vector<hipEvent_t> g_free_events;
+double g_total_ms[NVX_TIMER_COUNT] = {};
+int64_t g_count[NVX_TIMER_COUNT] = {};
+
+hipEvent_t take_event() {
+  if (!g_free_events.empty()) {
+    hipEvent_t e = g_free_events.back();
+    g_free_events.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Caller holds g_mu.
+int drain_locked() {
+  int rc = NVX_OK;
+  for (auto& p : g_pending) {
+    float ms = 0.f;
+    if (hipEventSynchronize(p.stop) != hipSuccess ||
+        hipEventElapsedTime(&ms, p.start, p.stop) != hipSuccess) {
+      rc = nvx::fail(NVX_EHIP, "timing: event elapsed time failed");
+    } else {
+      g_total_ms[p.id] += ms;
+      g_count[p.id] += 1;
+    }
+    g_free_events.push_back(p.start);
+    g_free_events.push_back(p.stop);
+  }
+  g_pending.clear();
+  return rc;
+}
+}  // namespace
+
+namespace nvx {
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+void clear_error() { g_err[0] = 0; }
+
+TimerScope::TimerScope(int id_, hipStream_t s) : id(id_), stream(s) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!g_timing) return;
+  start = take_event();
+  stop = take_event();
+  if (start && stop) (void)hipEventRecord(start, stream);
+}
+
+TimerScope::~TimerScope() {
+  if (!start || !stop) return;
+  std::lock_guard<std::mutex> lk(g_mu);
+  (void)hipEventRecord(stop, stream);
+  g_pending.push_back({id, start, stop});
+  // Bound the number of outstanding event pairs.
+  if (g_pending.size() > 4096) drain_locked();
+}
+
+}  // namespace nvx
+
+extern "C" {
+
+int nvx_version(void) { return 100; }
+
+const char* nvx_last_error(void) { return g_err; }
+
+int nvx_timing_enable(int on) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_timing = on != 0;
+  return NVX_OK;
+}
+
+int nvx_timing_read(int32_t kernel_id, double* total_ms, int64_t* count) {
+  NVX_CHECK(kernel_id >= 0 && kernel_id < NVX_TIMER_COUNT, "timing: bad kernel id %d", kernel_id);
+  std::lock_guard<std::mutex> lk(g_mu);
+  int rc = drain_locked();
+  if (total_ms) *total_ms = g_total_ms[kernel_id];
+  if (count) *count = g_count[kernel_id];
+  return rc;
+}
+
+int nvx_timing_reset(void) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  int rc = drain_locked();
+  for (int i = 0; i < NVX_TIMER_COUNT; ++i) {
+    g_total_ms[i] = 0;
+    g_count[i] = 0;
+  }
+  return rc;
+}
+
+}  // extern "C"

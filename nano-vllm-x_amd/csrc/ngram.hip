@@ -1,0 +1,92 @@
+// N-gram prompt-lookup drafter (integer only, one workgroup per history).
+//
+// A window h[e-n:e] (e = exclusive end) matches the length-n suffix iff
+// h[e-t] == h[L-t] for t = 1..n.  Each thread computes, for the window ends it
+// owns, the backward match length ml(e) (capped at the largest usable n) and keeps
+// best[n] = smallest e with ml(e) >= n.  The proposal uses the largest n that has
+// any match and the smallest such e, which is the left-most window of that size:
+// the rule of transformers' PromptLookupCandidateGenerator.get_candidates
+// (generation/candidate_generator.py:1076-1096).  Only e <= L-1 qualifies (the
+// continuation must be non-empty).
+#include "nvx_internal.h"
+
+namespace {
+
+constexpr int kNT = 256;
+constexpr int kMaxNgram = 8;
+
+__global__ __launch_bounds__(kNT) void ngram_kernel(const int32_t* __restrict__ tokens,
+                                                    const int64_t* __restrict__ offsets,
+                                                    int min_n, int max_n, int k,
+                                                    int32_t* __restrict__ draft,
+                                                    int32_t* __restrict__ draft_len) {
+  __shared__ int red[kNT / nvx::kWave];
+  const int b = blockIdx.x;
+  const int64_t off = offsets[b];
+  const int64_t L64 = offsets[b + 1] - off;
+  const int L = (int)L64;
+  const int32_t* h = tokens + off;
+  const int nmax = min(max_n, L - 1);
+
+  int32_t* out = draft + (int64_t)b * k;
+  if (nmax < min_n) {  // uniform across the block
+    for (int j = threadIdx.x; j < k; j += kNT) out[j] = -1;
+    if (threadIdx.x == 0) draft_len[b] = 0;
+    return;
+  }
+
+  int32_t suf[kMaxNgram];
+#pragma unroll
+  for (int t = 0; t < kMaxNgram; ++t) suf[t] = (t < nmax) ? h[L - 1 - t] : 0;
+
+  int best[kMaxNgram + 1];
+#pragma unroll
+  for (int n = 0; n <= kMaxNgram; ++n) best[n] = INT32_MAX;
+  int local_max = 0;
+
+  for (int e = 1 + threadIdx.x; e <= L - 1; e += kNT) {
+    int ml = 0;
+#pragma unroll
+    for (int t = 0; t < kMaxNgram; ++t) {
+      if (t < nmax && ml == t && e - 1 - t >= 0 && h[e - 1 - t] == suf[t]) ml = t + 1;
+    }
+    local_max = max(local_max, ml);
+#pragma unroll
+    for (int n = 1; n <= kMaxNgram; ++n)
+      if (ml >= n && e < best[n]) best[n] = e;
+  }
+
+  const int nstar = nvx::block_max_i<kNT>(local_max, red);
+  int e_star = -1;
+  if (nstar >= min_n) {
+    int mine = INT32_MAX;
+#pragma unroll
+    for (int n = 1; n <= kMaxNgram; ++n)
+      if (n == nstar) mine = best[n];
+    e_star = nvx::block_min_i<kNT>(mine, red);
+  }
+  const int len = (e_star < 0) ? 0 : min(k, L - e_star);
+  for (int j = threadIdx.x; j < k; j += kNT) out[j] = (j < len) ? h[e_star + j] : -1;
+  if (threadIdx.x == 0) draft_len[b] = len;
+}
+
+}  // namespace
+
+extern "C" int nvx_ngram_propose(const int32_t* tokens, const int64_t* offsets, int32_t num_seqs,
+                                 int32_t min_ngram, int32_t max_ngram, int32_t num_draft,
+                                 int32_t* draft, int32_t* draft_len, void* stream) {
+  nvx::clear_error();
+  NVX_CHECK(num_seqs >= 0, "ngram_propose: num_seqs must be >= 0 (got %d)", num_seqs);
+  NVX_CHECK(min_ngram >= 1 && min_ngram <= max_ngram && max_ngram <= kMaxNgram,
+            "ngram_propose: need 1 <= min_ngram <= max_ngram <= %d (got %d, %d)", kMaxNgram,
+            min_ngram, max_ngram);
+  NVX_CHECK(num_draft >= 1, "ngram_propose: num_draft must be >= 1 (got %d)", num_draft);
+  if (num_seqs == 0) return NVX_OK;
+  NVX_CHECK(tokens && offsets && draft && draft_len, "ngram_propose: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  nvx::TimerScope timer(NVX_TIMER_NGRAM, s);
+  hipLaunchKernelGGL(ngram_kernel, dim3(num_seqs), dim3(kNT), 0, s, tokens, offsets, min_ngram,
+                     max_ngram, num_draft, draft, draft_len);
+  NVX_LAUNCHED();
+  return NVX_OK;
+}

@@ -1,0 +1,111 @@
+"""Attention layer and KV-cache scatter on libnvx_spec (gfx950 HIP kernels).
+
+Drop-in for the reference's nanovllm/layers/attention.py:
+  * ``store_kvcache(key, value, k_cache, v_cache, slot_mapping)`` keeps the
+    signature and the asserts of attention.py:33-40 (the Triton kernel at :10-30
+    becomes ``nvx_store_kvcache``).
+  * ``Attention(num_heads, head_dim, scale, num_kv_heads)`` keeps attention.py:43-75:
+    ``forward(q, k, v)`` stores K/V into the bound cache, then attends.  Decode and
+    the speculative verify step call ``tree_attention`` (q_len rows per sequence,
+    ancestor mask from the context; without a mask the rule is causal, which for
+    q_len = 1 is the reference's decode call at :71-74).  Prefill attends over the
+    paged cache with the causal rule, which covers both branches of :64-70 since the
+    prompt's K/V are stored first.
+"""
+import torch
+from torch import nn
+
+from .. import _C
+from ..utils.context import get_context
+
+def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                  v_cache: torch.Tensor, slot_mapping: torch.Tensor):
+    N, num_heads, head_dim = key.shape
+    D = num_heads * head_dim
+    assert key.stride(-1) == 1 and value.stride(-1) == 1
+    assert key.stride(1) == head_dim and value.stride(1) == head_dim
+    assert k_cache.stride(1) == D and v_cache.stride(1) == D
+    assert slot_mapping.numel() == N
+    assert key.dtype == value.dtype == k_cache.dtype == v_cache.dtype
+    assert slot_mapping.dtype == torch.int32
+    _C.require_cuda(key, value, k_cache, v_cache, slot_mapping)
+    es = key.element_size()
+    _C.check(_C.lib().nvx_store_kvcache(
+        _C.ptr(key), key.stride(0) * es, _C.ptr(value), value.stride(0) * es,
+        _C.ptr(k_cache), _C.ptr(v_cache), _C.ptr(slot_mapping), N, D * es, _C.stream_of(key)))
+
+
+def tree_attention(q, k_cache, v_cache, block_tables, cu_seqlens_q, context_lens, scale,
+                   tree_mask=None, max_seqlen_q=None, max_context_len=None, out=None):
+    """Paged attention of each sequence's q rows against its cached context.
+
+    q: bf16 [N, Hq, 128]; caches: bf16 [num_blocks, block_size, Hkv, 128];
+    block_tables int32 [B, max_blocks]; cu_seqlens_q int32 [B+1]; context_lens int32 [B]
+    (including the q rows, which must already be stored); tree_mask: int64/uint64 [N]
+    ancestor bitmask or None (causal).  Returns bf16 [N, Hq, 128].
+    """
+    N, Hq, D = q.shape
+    nblk, bs, Hkv, Dk = k_cache.shape
+    if D != Dk or v_cache.shape != k_cache.shape:
+        raise ValueError(f"tree_attention: q {tuple(q.shape)} vs cache {tuple(k_cache.shape)}")
+    if q.dtype != torch.bfloat16 or k_cache.dtype != torch.bfloat16:
+        raise ValueError("tree_attention: q and the caches must be bfloat16")
+    if not (q.is_contiguous() and k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("tree_attention: q and the caches must be contiguous")
+    for name, t in (("block_tables", block_tables), ("cu_seqlens_q", cu_seqlens_q),
+                    ("context_lens", context_lens)):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise ValueError(f"tree_attention: {name} must be contiguous int32")
+    if tree_mask is not None and (tree_mask.dtype not in (torch.int64, torch.uint64)
+                                  or tree_mask.numel() != N or not tree_mask.is_contiguous()):
+        raise ValueError("tree_attention: tree_mask must be a contiguous 64-bit tensor with "
+                         "one entry per q row")
+    _C.require_cuda(q, k_cache, v_cache, block_tables, cu_seqlens_q, context_lens, tree_mask)
+    B = context_lens.numel()
+    if max_seqlen_q is None:
+        max_seqlen_q = int((cu_seqlens_q[1:] - cu_seqlens_q[:-1]).max().item()) if B else 0
+    if max_context_len is None:
+        max_context_len = int(context_lens.max().item()) if B else 0
+    o = torch.empty_like(q) if out is None else out
+    L = _C.lib()
+    ws_bytes = L.nvx_tree_attention_workspace_size(B, N, max_seqlen_q, max_context_len, Hq, Hkv, D)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+    _C.check(L.nvx_tree_attention(
+        _C.ptr(q), _C.ptr(o), _C.ptr(k_cache), _C.ptr(v_cache), _C.ptr(block_tables),
+        block_tables.shape[1] if block_tables.dim() == 2 else 1, _C.ptr(cu_seqlens_q),
+        _C.ptr(context_lens), _C.ptr(tree_mask), B, N, max_seqlen_q, max_context_len, Hq, Hkv, D,
+        bs, float(scale), _C.ptr(ws), ws_bytes, _C.stream_of(q)))
+    return o
+
+
+class Attention(nn.Module):
+
+    def __init__(self, num_heads, head_dim, scale, num_kv_heads):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.scale = scale
+        self.num_kv_heads = num_kv_heads
+        self.k_cache = self.v_cache = torch.tensor([])
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
+        context = get_context()
+        k_cache, v_cache = self.k_cache, self.v_cache
+        if not (k_cache.numel() and v_cache.numel()):
+            raise RuntimeError("Attention: the paged KV cache is not bound (ModelRunner binds "
+                               "k_cache/v_cache before the first forward)")
+        store_kvcache(k, v, k_cache, v_cache, context.slot_mapping)
+        q = q.contiguous()
+        if context.is_prefill:
+            cu_q, ctx_lens = context.cu_seqlens_q, context.context_lens
+            if ctx_lens is None:
+                ctx_lens = (context.cu_seqlens_k[1:] - context.cu_seqlens_k[:-1]).to(torch.int32)
+            return tree_attention(q, k_cache, v_cache, context.block_tables, cu_q, ctx_lens,
+                                  self.scale, None, context.max_seqlen_q,
+                                  context.max_seqlen_k)
+        cu_q = context.cu_seqlens_q
+        if cu_q is None:  # plain decode: one q row per sequence
+            cu_q = torch.arange(q.shape[0] + 1, dtype=torch.int32, device=q.device)
+        return tree_attention(q, k_cache, v_cache, context.block_tables, cu_q,
+                              context.context_lens, self.scale, context.tree_mask,
+                              context.max_seqlen_q or None, context.max_context_len or None)

@@ -1,0 +1,143 @@
+"""Sampler and speculative rejection sampler on libnvx_spec (gfx950 HIP kernels).
+
+* ``temperature_softmax`` -- fp32 ``softmax(logits.float() / T)`` per row, the first
+  two lines of the reference's ``Sampler.forward`` (nanovllm/layers/sampler.py:9-10).
+  Rows with temperature 0 are greedy and keep their fp32 logits.
+* ``Sampler()(logits, temperatures)`` -- drop-in for sampler.py:5-12: one categorical
+  draw per row (an inverse-CDF draw with device uniforms instead of the reference's
+  exponential race; same distribution).  Greedy rows (temperature 0) take the argmax,
+  which the reference forbids at sampling_params.py:11.
+* ``rejection_sample_tree`` / ``rejection_sample_chain`` / ``RejectionSampler`` --
+  speculative verification of a draft tree / chain (absent in the reference).
+"""
+import torch
+from torch import nn
+
+from .. import _C
+
+_DTYPE_CODE = {torch.float32: _C.DTYPE_F32, torch.bfloat16: _C.DTYPE_BF16}
+
+
+def temperature_softmax(logits: torch.Tensor, temperatures: torch.Tensor, out=None):
+    """logits [N, V] (fp32 or bf16, unit stride in V); temperatures fp32 [N]."""
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("temperature_softmax: logits must be [N, V] with unit stride in V")
+    if logits.dtype not in _DTYPE_CODE:
+        raise ValueError(f"temperature_softmax: unsupported logits dtype {logits.dtype}")
+    N, V = logits.shape
+    temperatures = temperatures.to(device=logits.device, dtype=torch.float32).contiguous()
+    if temperatures.numel() != N:
+        raise ValueError("temperature_softmax: one temperature per row")
+    probs = torch.empty(N, V, dtype=torch.float32, device=logits.device) if out is None else out
+    _C.require_cuda(logits, temperatures, probs)
+    _C.check(_C.lib().nvx_temperature_softmax(
+        _C.ptr(logits), _DTYPE_CODE[logits.dtype], logits.stride(0), _C.ptr(temperatures),
+        _C.ptr(probs), N, V, _C.stream_of(logits)))
+    return probs
+
+
+def _i32(t):
+    return t.to(torch.int32).contiguous()
+
+
+def rejection_sample_tree(target_probs, draft_probs, tokens, parents, uniforms, final_uniforms,
+                          greedy=None, num_nodes=None, draft_mode="stochastic"):
+    """Verify one draft tree per sequence.
+
+    target_probs fp32 [B, T, V] (row i: target distribution after node i);
+    draft_probs fp32 [B, T', V] (row i: distribution that proposed node i's children,
+    T' >= number of internal-node rows used) or None with draft_mode="delta";
+    tokens, parents int [B, T] (parents[:, 0] = -1, parents[b, i] < i);
+    uniforms fp32 [B, T]; final_uniforms fp32 [B]; greedy bool [B] or None;
+    num_nodes int [B] or None (ragged trees).
+
+    Returns int32 (path [B, T], accepted_len [B], out_tokens [B, T], next_token [B]).
+    """
+    B, T, V = target_probs.shape
+    if target_probs.dtype != torch.float32 or target_probs.stride(2) != 1 \
+            or target_probs.stride(1) != V:
+        raise ValueError("rejection_sample_tree: target_probs must be fp32 with contiguous rows")
+    delta = draft_mode == "delta"
+    if not delta:
+        if draft_probs is None or draft_probs.dtype != torch.float32 or \
+                draft_probs.stride(2) != 1 or draft_probs.stride(1) != V or draft_probs.shape[2] != V:
+            raise ValueError("rejection_sample_tree: draft_probs must be fp32 [B, T', V] with "
+                             "contiguous rows")
+    if T > 64:
+        raise ValueError("rejection_sample_tree: at most 64 nodes per tree")
+    dev = target_probs.device
+    tokens, parents = _i32(tokens), _i32(parents)
+    uniforms = uniforms.to(torch.float32).contiguous()
+    final_uniforms = final_uniforms.to(torch.float32).contiguous()
+    g = None if greedy is None else greedy.to(device=dev, dtype=torch.uint8).contiguous()
+    nn_ = None if num_nodes is None else _i32(num_nodes)
+    path = torch.empty(B, T, dtype=torch.int32, device=dev)
+    acc = torch.empty(B, dtype=torch.int32, device=dev)
+    out_tokens = torch.empty(B, T, dtype=torch.int32, device=dev)
+    nxt = torch.empty(B, dtype=torch.int32, device=dev)
+    _C.require_cuda(target_probs, draft_probs, tokens, parents, uniforms, final_uniforms, g, nn_)
+    _C.check(_C.lib().nvx_rejection_sample_tree(
+        _C.ptr(target_probs), target_probs.stride(0), None if delta else _C.ptr(draft_probs),
+        0 if delta else draft_probs.stride(0), V, _C.ptr(tokens), _C.ptr(parents), _C.ptr(nn_), T,
+        _C.ptr(uniforms), _C.ptr(final_uniforms), _C.ptr(g), 1 if delta else 0, B, _C.ptr(path),
+        _C.ptr(acc), _C.ptr(out_tokens), _C.ptr(nxt), _C.stream_of(target_probs)))
+    return path, acc, out_tokens, nxt
+
+
+def rejection_sample_chain(target_probs, draft_probs, draft_token_ids, uniforms, final_uniforms,
+                           greedy=None):
+    """Chain speculative sampling (Leviathan et al. 2023, Alg. 1).
+
+    target_probs fp32 [B, k+1, V]; draft_probs fp32 [B, k, V]; draft_token_ids [B, k];
+    uniforms [B, k]; final_uniforms [B].  Returns int32 (accepted_len [B],
+    recovered [B] (-1 when every draft token was accepted), bonus [B] (-1 otherwise),
+    tokens [B, k+1] (accepted tokens then the recovered/bonus token, -1 padded)).
+    """
+    B, k1, V = target_probs.shape
+    k = k1 - 1
+    dev = target_probs.device
+    tok = torch.zeros(B, k1, dtype=torch.int32, device=dev)
+    tok[:, 1:] = draft_token_ids.to(torch.int32)
+    u = torch.zeros(B, k1, dtype=torch.float32, device=dev)
+    u[:, 1:] = uniforms
+    parents = (torch.arange(k1, dtype=torch.int32, device=dev) - 1).expand(B, k1).contiguous()
+    _, acc, toks, nxt = rejection_sample_tree(target_probs, draft_probs, tok, parents, u,
+                                              final_uniforms, greedy)
+    full = acc == k
+    recovered = torch.where(full, torch.full_like(nxt, -1), nxt)
+    bonus = torch.where(full, nxt, torch.full_like(nxt, -1))
+    return acc, recovered, bonus, toks
+
+
+class Sampler(nn.Module):
+    """Sampler()(logits [N, V], temperatures [N]) -> int64 token ids [N]."""
+
+    def forward(self, logits: torch.Tensor, temperatures: torch.Tensor, uniforms=None):
+        N, V = logits.shape
+        probs = temperature_softmax(logits, temperatures)
+        dev = logits.device
+        u = torch.rand(N, device=dev) if uniforms is None else uniforms
+        zeros = torch.zeros(N, 1, dtype=torch.int32, device=dev)
+        greedy = temperatures.to(dev) == 0
+        _, _, _, nxt = rejection_sample_tree(probs.view(N, 1, V), None, zeros, zeros - 1,
+                                             zeros.float(), u, greedy, draft_mode="delta")
+        return nxt.long()
+
+
+class RejectionSampler(nn.Module):
+    """Temperature softmax of the target logits followed by tree verification.
+
+    forward(target_logits [B*T, V], temperatures [B], draft_probs [B, T, V] | None,
+    tokens [B, T], parents [B, T], uniforms [B, T], final_uniforms [B]) ->
+    (path, accepted_len, out_tokens, next_token), int32.
+    """
+
+    def forward(self, target_logits, temperatures, draft_probs, tokens, parents, uniforms,
+                final_uniforms, num_nodes=None):
+        B, T = tokens.shape
+        V = target_logits.shape[-1]
+        temps = temperatures.to(device=target_logits.device, dtype=torch.float32)
+        probs = temperature_softmax(target_logits.view(B * T, V), temps.repeat_interleave(T))
+        return rejection_sample_tree(probs.view(B, T, V), draft_probs, tokens, parents, uniforms,
+                                     final_uniforms, temps == 0, num_nodes,
+                                     "delta" if draft_probs is None else "stochastic")

@@ -1,0 +1,96 @@
+"""Seeded synthetic workloads for the verify path (host-side, numpy/torch CPU).
+
+Integer data comes from numpy PCG64 generators, float tensors from a seeded CPU
+torch.Generator; everything is generated on the host and then copied to the GPU
+so the HIP kernels and the CPU restatement see identical inputs.
+"""
+import numpy as np
+import torch
+
+from ..spec.tree import ancestor_masks, depths, random_tree
+
+
+def ngram_histories(num_seqs, min_len, max_len, vocab, rng, copy_frac=0.30, span=(8, 32)):
+    """Token histories with lengths U[min_len, max_len], ids U[0, vocab); spans of
+    length U[span] are copied from an earlier start to a later start until
+    >= copy_frac of the positions were overwritten."""
+    out = []
+    for _ in range(num_seqs):
+        L = int(rng.integers(min_len, max_len + 1))
+        h = rng.integers(0, vocab, size=L, dtype=np.int64).astype(np.int32)
+        covered = np.zeros(L, dtype=bool)
+        target = copy_frac * L
+        guard = 0
+        while covered.sum() < target and guard < 100000:
+            guard += 1
+            n = int(rng.integers(span[0], span[1] + 1))
+            if L < 2 * n + 1:
+                break
+            dst = int(rng.integers(n, L - n + 1))
+            src = int(rng.integers(0, dst - n + 1))
+            h[dst:dst + n] = h[src:src + n]
+            covered[dst:dst + n] = True
+        out.append(h)
+    return out
+
+
+def pack_histories(hist):
+    offs = np.zeros(len(hist) + 1, dtype=np.int64)
+    offs[1:] = np.cumsum([len(h) for h in hist])
+    flat = np.concatenate(hist) if hist else np.zeros(0, np.int32)
+    return flat.astype(np.int32), offs
+
+
+def paged_block_tables(seq_lens, block_size, rng, extra_blocks=0):
+    """Block tables placing each sequence's pages at random physical blocks
+    (a random permutation of the pool).  Returns (int32 [B, max_blocks] padded -1,
+    number of physical blocks)."""
+    nb = [(int(n) + block_size - 1) // block_size for n in seq_lens]
+    total = sum(nb) + extra_blocks
+    perm = rng.permutation(total).astype(np.int32)
+    width = max(nb) if nb else 1
+    bt = np.full((len(seq_lens), max(width, 1)), -1, dtype=np.int32)
+    k = 0
+    for b, n in enumerate(nb):
+        bt[b, :n] = perm[k:k + n]
+        k += n
+    return bt, total
+
+
+def slots_for(bt_row, positions, block_size):
+    positions = np.asarray(positions, dtype=np.int64)
+    return (np.asarray(bt_row, np.int64)[positions // block_size] * block_size
+            + positions % block_size).astype(np.int32)
+
+
+class VerifyBatch:
+    """Inputs of one verify step: B sequences with ctx cached tokens and a
+    T-node draft tree each."""
+
+    def __init__(self, ctx_lens, trees, block_size, rng):
+        self.B = len(ctx_lens)
+        self.ctx = np.asarray(ctx_lens, dtype=np.int32)
+        self.parents = [np.asarray(p, np.int32) for p in trees]
+        self.qlens = np.array([len(p) for p in trees], dtype=np.int32)
+        self.T = int(self.qlens.max())
+        self.block_size = block_size
+        self.bt, self.num_blocks = paged_block_tables(self.ctx + self.qlens, block_size, rng)
+        self.cu_q = np.zeros(self.B + 1, dtype=np.int32)
+        self.cu_q[1:] = np.cumsum(self.qlens)
+        self.context_lens = (self.ctx + self.qlens).astype(np.int32)
+        self.masks = (np.concatenate([ancestor_masks(p) for p in self.parents])
+                      if self.T <= 64 else None)
+        self.positions = np.concatenate([c + depths(p) for c, p in zip(self.ctx, self.parents)])
+        self.slot_mapping = np.concatenate([
+            slots_for(self.bt[b], self.ctx[b] + np.arange(self.qlens[b]), block_size)
+            for b in range(self.B)])
+
+    @classmethod
+    def random(cls, B, ctx_range, T, depth, block_size, rng):
+        ctx = rng.integers(ctx_range[0], ctx_range[1] + 1, size=B)
+        trees = [random_tree(T, depth, rng) for _ in range(B)]
+        return cls(ctx, trees, block_size, rng)
+
+
+def randn_bf16(shape, gen, std=1.0):
+    return (torch.randn(*shape, generator=gen) * std).to(torch.bfloat16)

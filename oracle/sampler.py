@@ -1,0 +1,262 @@
+"""Oracle: temperature softmax and chain/tree rejection sampling (fp32).
+
+Reference neighbour: nanovllm/layers/sampler.py:9-11 -- ``logits.float() /
+temperature``, ``softmax(dim=-1)``, then a categorical draw.  The reference has no
+rejection sampler and cannot take injected uniforms (its draw uses device RNG), so
+the contract below is restated from the published algorithms:
+
+* chain: Leviathan et al. 2023, Algorithm 1 (arXiv:2211.17192) -- accept draft
+  token x with probability min(1, p(x)/q(x)); on rejection draw from
+  norm(max(p - q, 0)); if every draft token is accepted draw a bonus token from p.
+* tree: SpecInfer multi-step speculative sampling -- at the current node, test its
+  children in ascending node order against the current distribution; each
+  rejection replaces it by norm(max(cur - q, 0)); an accepted child becomes the
+  current node with distribution P[child].
+
+Exact fp32 contract (shared with the HIP kernel so integer outputs are bit-exact):
+
+* acceptance of child c with token x: ``U[c] * q[x] <= cur[x] and cur[x] > 0``
+  (``q[x]`` is 1 in delta mode, where the children are deterministic proposals);
+* residual step j: ``cur_j[y] = max(cur_{j-1}[y] - q[y], 0) / S_j`` (delta mode:
+  ``cur_j[y] = (y == x_j ? 0 : cur_{j-1}[y]) / S_j``), with ``S_j`` the
+  ``canonical_sum`` of the un-normalised residual; if ``S_j`` is not > 0 the
+  distribution falls back to ``P[cur]``;
+* the final token is ``cdf_pick(cur, U_final)``;
+* greedy rows (temperature 0): child accepted iff its token equals the first
+  index of the maximum of the row; otherwise the next token is that index.
+
+``canonical_sum`` and ``cdf_pick`` fix the fp32 association order: 1024 lanes
+(16 wave64s).  For the sum, lane t accumulates, in order, the 4-element groups
+t, t+1024, t+2048, ... (elements 4g..4g+3 in ascending order), then each wave
+combines lanes with an xor butterfly (offsets 32..1) and wave totals combine with
+an xor butterfly over 16 (offsets 8..1).  For the pick, lane t owns the contiguous
+chunk [t*C, (t+1)*C) with C = 4*ceil(ceil(V/4)/1024); chunk sums are scanned with a
+Kogge-Stone inclusive scan inside each wave (offsets 1..32) and across the 16 wave
+totals (offsets 1..8).
+
+Pinned by (tests/test_oracle_sampler.py): Q=P always accepts; disjoint supports
+always reject; the output distribution enumerated over uniform grids on tiny
+vocabularies equals P; chain sampling agrees in distribution with transformers'
+``_speculative_sampling`` (generation/utils.py:3992); canonical_sum agrees with
+math.fsum; cdf_pick agrees with a float64 searchsorted away from CDF steps;
+committed golden fixtures under tests/golden/.
+"""
+import numpy as np
+
+LANES = 1024
+WAVE = 64
+NWAVES = LANES // WAVE
+F32 = np.float32
+
+
+# --------------------------------------------------------------------------- softmax
+def temperature_softmax(logits, temperatures):
+    """softmax(logits.float() / T) per row (reference sampler.py:9-10).
+
+    Rows with temperature 0 (greedy) return the fp32 logits unchanged: only their
+    argmax is used.  Computed in float64 and rounded, so it is the correctly
+    rounded target the fp32 kernel is compared against (1e-5 relative).
+    """
+    x32 = np.asarray(logits, dtype=F32)
+    t32 = np.asarray(temperatures, dtype=F32).reshape(-1, 1)
+    greedy = t32[:, 0] == 0
+    # logits.float().div_(T) is one correctly rounded fp32 division (sampler.py:9);
+    # exp and the normalisation are then done in float64.
+    xs = (x32 / np.where(greedy[:, None], F32(1), t32)).astype(np.float64)
+    m = xs.max(axis=1, keepdims=True)
+    e = np.exp(xs - m)
+    p = e / e.sum(axis=1, keepdims=True)
+    out = p.astype(F32)
+    out[greedy] = x32[greedy]
+    return out
+
+
+# ------------------------------------------------------------ canonical reductions
+def _cdiv(a, b):
+    return -(-a // b)
+
+
+def _xor_butterfly(a, offsets):
+    idx = np.arange(a.shape[-1])
+    for off in offsets:
+        a = a + a[..., idx ^ off]
+    return a
+
+
+def _kogge_stone(a, offsets):
+    a = a.copy()
+    n = a.shape[-1]
+    for off in offsets:
+        b = a.copy()
+        b[..., off:] = a[..., off:] + a[..., :n - off]
+        a = b
+    return a
+
+
+def canonical_sum(row):
+    row = np.asarray(row, dtype=F32)
+    V = row.shape[0]
+    R = _cdiv(_cdiv(V, 4), LANES)
+    pad = np.zeros(R * LANES * 4, dtype=F32)
+    pad[:V] = row
+    X = pad.reshape(R, LANES, 4)
+    acc = np.zeros(LANES, dtype=F32)
+    for r in range(R):
+        for c in range(4):
+            acc = acc + X[r, :, c]
+    w = _xor_butterfly(acc.reshape(NWAVES, WAVE), (32, 16, 8, 4, 2, 1))[:, 0]
+    return F32(_xor_butterfly(w, (8, 4, 2, 1))[0])
+
+
+def cdf_pick(row, u):
+    """First x with F(x) > u*total and row[x] > 0 (fallback: last x with row[x] > 0)."""
+    row = np.asarray(row, dtype=F32)
+    V = row.shape[0]
+    C = 4 * _cdiv(_cdiv(V, 4), LANES)
+    pad = np.zeros(C * LANES, dtype=F32)
+    pad[:V] = row
+    X = pad.reshape(LANES, C)
+    s = np.zeros(LANES, dtype=F32)
+    for j in range(C):
+        s = s + X[:, j]
+    incl_w = _kogge_stone(s.reshape(NWAVES, WAVE), (1, 2, 4, 8, 16, 32))
+    wt = _kogge_stone(incl_w[:, -1], (1, 2, 4, 8))
+    incl = incl_w.copy()
+    incl[1:] = wt[:-1, None] + incl_w[1:]
+    incl = incl.reshape(LANES)
+    total = wt[-1]
+    tau = F32(F32(u) * total)
+    base = np.zeros(LANES, dtype=F32)
+    base[1:] = incl[:-1]
+    F = np.empty((LANES, C), dtype=F32)
+    run = base.copy()
+    for j in range(C):
+        run = run + X[:, j]
+        F[:, j] = run
+    hit = ((F > tau) & (X > 0)).reshape(-1)[:V]
+    nz = np.nonzero(hit)[0]
+    if nz.size:
+        return int(nz[0])
+    pos = np.nonzero(row > 0)[0]
+    return int(pos[-1]) if pos.size else -1
+
+
+def first_argmax(row):
+    return int(np.argmax(np.asarray(row, dtype=F32)))
+
+
+# ------------------------------------------------------------------- tree sampling
+class _Chain:
+    """Residual chain cur_0 = p, cur_j = step_j(cur_{j-1})."""
+
+    def __init__(self, p, q, delta):
+        self.p, self.q, self.delta = p, q, delta
+        self.steps = []  # (S_j, x_j); S_j <= 0 means fall back to p
+
+    def eval(self, ys=None):
+        v = self.p if ys is None else self.p[ys]
+        for S, x in self.steps:
+            if not S > 0:
+                v = self.p if ys is None else self.p[ys]
+                continue
+            if self.delta:
+                yy = np.arange(self.p.shape[0]) if ys is None else ys
+                v = np.where(yy == x, F32(0), v) / S
+            else:
+                qq = self.q if ys is None else self.q[ys]
+                v = np.maximum(v - qq, F32(0)) / S
+        return v.astype(F32)
+
+    def reject(self, x):
+        cur = self.eval()
+        if self.delta:
+            r = cur.copy()
+            if 0 <= x < r.shape[0]:
+                r[x] = 0
+        else:
+            r = np.maximum(cur - self.q, F32(0))
+        self.steps.append((canonical_sum(r), x))
+
+
+def sample_tree_one(P, Q, tokens, parents, U, u_final, greedy, delta=False):
+    """One sequence.  P: [T, V] fp32 target rows, Q: [T, V] fp32 draft rows (ignored
+    in delta and greedy modes), tokens/parents/U: [T].  Returns
+    (path list of node ids starting at 0, next token)."""
+    T = len(parents)
+    children = [[] for _ in range(T)]
+    for j in range(1, T):
+        children[int(parents[j])].append(j)
+    cur, path = 0, [0]
+    while True:
+        kids = children[cur]
+        if greedy:
+            a = first_argmax(P[cur])
+            nxt = next((c for c in kids if int(tokens[c]) == a), None)
+            if nxt is None:
+                return path, a
+            cur = nxt
+            path.append(cur)
+            continue
+        p = np.asarray(P[cur], dtype=F32)
+        q = None if delta else np.asarray(Q[cur], dtype=F32)
+        chain = _Chain(p, q, delta)
+        accepted = None
+        V = p.shape[0]
+        for c in kids:
+            x = int(tokens[c])
+            if 0 <= x < V:  # a token outside the vocabulary is rejected
+                cx = chain.eval(np.array([x]))[0]
+                qx = F32(1) if delta else q[x]
+                if F32(F32(U[c]) * qx) <= cx and cx > 0:
+                    accepted = c
+                    break
+            chain.reject(x)
+        if accepted is None:
+            return path, cdf_pick(chain.eval(), u_final)
+        cur = accepted
+        path.append(cur)
+
+
+def rejection_sample_tree(P, Q, tokens, parents, U, U_final, greedy, num_nodes=None,
+                          delta=False):
+    """Batched oracle.  P, Q: [B, T, V]; tokens, parents, U: [B, T]; U_final, greedy: [B].
+
+    Returns (path [B, T] int32 padded -1, accepted_len [B], out_tokens [B, T] int32
+    (accepted tokens then the next token, padded -1), next_token [B])."""
+    P = np.asarray(P, dtype=F32)
+    B, T = np.asarray(parents).shape
+    path_o = np.full((B, T), -1, np.int32)
+    acc_o = np.zeros(B, np.int32)
+    tok_o = np.full((B, T), -1, np.int32)
+    nxt_o = np.zeros(B, np.int32)
+    for b in range(B):
+        n = T if num_nodes is None else int(num_nodes[b])
+        path, nxt = sample_tree_one(P[b, :n], None if Q is None else Q[b, :n],
+                                    tokens[b, :n], parents[b, :n], U[b, :n], U_final[b],
+                                    bool(greedy[b]), delta)
+        path_o[b, :len(path)] = path
+        acc_o[b] = len(path) - 1
+        toks = [int(tokens[b, i]) for i in path[1:]] + [nxt]
+        tok_o[b, :len(toks)] = toks
+        nxt_o[b] = nxt
+    return path_o, acc_o, tok_o, nxt_o
+
+
+def rejection_sample_chain(P, Q, draft_tokens, U, U_final, greedy):
+    """Chain special case (parents[i] = i-1).  P: [B, k+1, V], Q: [B, k, V],
+    draft_tokens / U: [B, k].  Returns (accepted_len [B], recovered [B] (-1 if every
+    draft token was accepted), bonus [B] (-1 otherwise), tokens [B, k+1])."""
+    P = np.asarray(P, dtype=F32)
+    B, k1, V = P.shape
+    k = k1 - 1
+    Qp = np.zeros((B, k1, V), F32)
+    Qp[:, :k] = Q
+    tok = np.zeros((B, k1), np.int32)
+    tok[:, 1:] = draft_tokens
+    Up = np.zeros((B, k1), F32)
+    Up[:, 1:] = U
+    parents = np.tile(np.arange(-1, k, dtype=np.int32), (B, 1))
+    _, acc, toks, nxt = rejection_sample_tree(P, Qp, tok, parents, Up, U_final, greedy)
+    recovered = np.where(acc < k, nxt, -1).astype(np.int32)
+    bonus = np.where(acc == k, nxt, -1).astype(np.int32)
+    return acc, recovered, bonus, toks

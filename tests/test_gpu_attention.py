@@ -1,0 +1,147 @@
+"""Tree attention (HIP) vs the CPU oracle: within 2e-2 absolute in bf16."""
+import numpy as np
+import pytest
+import torch
+
+from nanovllm.layers.attention import store_kvcache, tree_attention, Attention
+from nanovllm.spec.tree import chain_parents, random_tree
+from nanovllm.utils.context import set_context, reset_context
+from nanovllm.utils.synthetic import VerifyBatch, randn_bf16
+from oracle import attention as oatt
+
+TOL = 2e-2
+
+
+def run_case(dev, Hq, Hkv, ctx, trees, seed, block_size=256, causal=False):
+    rng = np.random.default_rng(seed)
+    g = torch.Generator().manual_seed(seed)
+    vb = VerifyBatch(ctx, trees, block_size, rng)
+    D = 128
+    kc = randn_bf16((vb.num_blocks, block_size, Hkv, D), g)
+    vc = randn_bf16((vb.num_blocks, block_size, Hkv, D), g)
+    N = int(vb.cu_q[-1])
+    q = randn_bf16((N, Hq, D), g)
+    mask = None if causal else torch.from_numpy(vb.masks)
+    print(f"[attn] Hq={Hq} Hkv={Hkv} B={vb.B} N={N} maxctx={int(vb.context_lens.max())} "
+          f"causal={causal} seed={seed}", flush=True)
+    o = tree_attention(q.to(dev), kc.to(dev), vc.to(dev), torch.from_numpy(vb.bt).to(dev),
+                       torch.from_numpy(vb.cu_q).to(dev), torch.from_numpy(vb.context_lens).to(dev),
+                       D ** -0.5, None if mask is None else mask.to(dev))
+    ref = oatt.paged_attention(q.float().numpy(), kc.float().numpy(), vc.float().numpy(), vb.bt,
+                               vb.cu_q, vb.context_lens,
+                               None if causal else vb.masks.view(np.uint64), D ** -0.5, block_size)
+    err = np.abs(o.cpu().float().numpy() - ref)
+    assert np.isfinite(o.cpu().float().numpy()).all()
+    assert err.max() < TOL, f"max abs err {err.max()}"
+    return err.max()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("Hq,Hkv", [(16, 8), (32, 8), (8, 8), (4, 1)])
+def test_small_trees(dev, Hq, Hkv):
+    rng = np.random.default_rng(1)
+    trees = [random_tree(t, d, rng) for t, d in ((8, 3), (32, 6), (1, 0), (17, 4))]
+    run_case(dev, Hq, Hkv, [300, 64, 5, 1000], trees, seed=Hq * 10 + Hkv)
+
+
+@pytest.mark.gpu
+def test_chain_equals_causal(dev):
+    rng = np.random.default_rng(2)
+    ctx = [700, 129]
+    trees = [chain_parents(6), chain_parents(20)]
+    run_case(dev, 16, 8, ctx, trees, seed=3)
+    run_case(dev, 16, 8, ctx, trees, seed=3, causal=True)
+
+
+@pytest.mark.gpu
+def test_decode_single_query(dev):
+    rng = np.random.default_rng(4)
+    ctx = list(rng.integers(1, 3000, size=37))
+    run_case(dev, 32, 8, ctx, [chain_parents(1)] * 37, seed=5)
+
+
+@pytest.mark.gpu
+def test_tree64_block512(dev):
+    rng = np.random.default_rng(6)
+    trees = [random_tree(64, 8, rng) for _ in range(3)]
+    run_case(dev, 32, 8, [2048, 100, 513], trees, seed=7, block_size=512)
+
+
+@pytest.mark.gpu
+def test_causal_prefill_long_queries(dev):
+    # prompt-style: q_len up to 300 with a cached prefix (multiple q-row chunks)
+    run_case(dev, 16, 8, [0, 256, 40], [chain_parents(300), chain_parents(77),
+                                         chain_parents(200)], seed=8, causal=True)
+
+
+@pytest.mark.gpu
+def test_config3_tree32_qwen3_0p6b(dev):
+    """Qwen3-0.6B shape: 16 q heads, 8 KV heads, B=32, ctx U[1024,4096], 32-node
+    depth-6 trees, pages scattered randomly (the split-KV path)."""
+    rng = np.random.default_rng(0)
+    ctx = rng.integers(1024, 4097, size=32)
+    trees = [random_tree(32, 6, rng) for _ in range(32)]
+    run_case(dev, 16, 8, ctx, trees, seed=0)
+
+
+@pytest.mark.gpu
+def test_config4_tree64_qwen3_8b_layer(dev):
+    """Qwen3-8B shape, one layer: 32 q heads, 8 KV heads, B=64, ctx 2048, 64-node
+    depth-8 trees (the single-split path)."""
+    rng = np.random.default_rng(1)
+    trees = [random_tree(64, 8, rng) for _ in range(64)]
+    run_case(dev, 32, 8, [2048] * 64, trees, seed=1)
+
+
+@pytest.mark.gpu
+def test_page_permutation_invariance(dev):
+    rng = np.random.default_rng(9)
+    g = torch.Generator().manual_seed(9)
+    trees = [random_tree(16, 4, rng) for _ in range(4)]
+    vb = VerifyBatch([500, 900, 33, 1500], trees, 256, rng)
+    kc = randn_bf16((vb.num_blocks, 256, 8, 128), g)
+    vc = randn_bf16((vb.num_blocks, 256, 8, 128), g)
+    q = randn_bf16((int(vb.cu_q[-1]), 16, 128), g).to(dev)
+    args = (torch.from_numpy(vb.cu_q).to(dev), torch.from_numpy(vb.context_lens).to(dev), 128 ** -0.5,
+            torch.from_numpy(vb.masks).to(dev))
+    o1 = tree_attention(q, kc.to(dev), vc.to(dev), torch.from_numpy(vb.bt).to(dev), *args)
+    perm = rng.permutation(vb.num_blocks)
+    inv = np.argsort(perm)
+    kc2, vc2 = kc[torch.from_numpy(perm)], vc[torch.from_numpy(perm)]
+    bt2 = np.where(vb.bt >= 0, inv[np.maximum(vb.bt, 0)], -1).astype(np.int32)
+    o2 = tree_attention(q, kc2.to(dev), vc2.to(dev), torch.from_numpy(bt2).to(dev), *args)
+    assert torch.equal(o1, o2)
+
+
+@pytest.mark.gpu
+def test_attention_module_store_then_attend(dev):
+    """Attention.forward: store the tree rows, then attend (reference order,
+    attention.py:62-74), driven through the Context side channel."""
+    rng = np.random.default_rng(10)
+    g = torch.Generator().manual_seed(10)
+    trees = [random_tree(12, 4, rng) for _ in range(3)]
+    vb = VerifyBatch([260, 31, 800], trees, 256, rng)
+    Hq, Hkv, D = 16, 8, 128
+    N = int(vb.cu_q[-1])
+    kc = randn_bf16((vb.num_blocks, 256, Hkv, D), g)
+    vc = randn_bf16((vb.num_blocks, 256, Hkv, D), g)
+    q, k, v = randn_bf16((N, Hq, D), g), randn_bf16((N, Hkv, D), g), randn_bf16((N, Hkv, D), g)
+    attn = Attention(Hq, D, D ** -0.5, Hkv)
+    attn.k_cache, attn.v_cache = kc.to(dev), vc.to(dev)
+    set_context(False, cu_seqlens_q=torch.from_numpy(vb.cu_q).to(dev),
+                slot_mapping=torch.from_numpy(vb.slot_mapping).to(dev),
+                context_lens=torch.from_numpy(vb.context_lens).to(dev),
+                block_tables=torch.from_numpy(vb.bt).to(dev),
+                tree_mask=torch.from_numpy(vb.masks).to(dev), max_seqlen_q=vb.T,
+                max_context_len=int(vb.context_lens.max()))
+    try:
+        o = attn(q.to(dev), k.to(dev), v.to(dev))
+    finally:
+        reset_context()
+    kf, vf = kc.float().numpy(), vc.float().numpy()
+    kff, vff = kf.reshape(-1, Hkv, D), vf.reshape(-1, Hkv, D)
+    kff[vb.slot_mapping] = k.float().numpy()
+    vff[vb.slot_mapping] = v.float().numpy()
+    ref = oatt.paged_attention(q.float().numpy(), kf, vf, vb.bt, vb.cu_q, vb.context_lens,
+                               vb.masks.view(np.uint64), D ** -0.5, 256)
+    assert np.abs(o.cpu().float().numpy() - ref).max() < TOL

@@ -1,0 +1,162 @@
+"""Sampler kernels (HIP) vs the CPU oracle.
+
+Softmax: within 1e-5 relative (fp32).  Rejection sampling: given the same fp32
+probabilities and uniforms, path / accepted length / tokens are bit-exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+from nanovllm.layers.sampler import (Sampler, rejection_sample_chain, rejection_sample_tree,
+                                     temperature_softmax)
+from nanovllm.spec.tree import chain_parents, random_tree
+from oracle import sampler as osamp
+
+V_QWEN = 151936
+
+
+def softmax_rows(gen, shape, std, temp):
+    return torch.softmax(torch.randn(*shape, generator=gen) * std / temp, -1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,V", [(torch.bfloat16, V_QWEN), (torch.float32, V_QWEN),
+                                     (torch.bfloat16, 1001), (torch.float32, 77)])
+def test_temperature_softmax(dev, dtype, V):
+    g = torch.Generator().manual_seed(V)
+    N = 24
+    logits = (torch.randn(N, V, generator=g) * 2).to(dtype)
+    temps = torch.tensor([1.0, 0.8, 0.0, 0.6, 1.7, 0.0] * 4)
+    print(f"[softmax] dtype={dtype} V={V}", flush=True)
+    p = temperature_softmax(logits.to(dev), temps.to(dev)).cpu().numpy()
+    ref = osamp.temperature_softmax(logits.float().numpy(), temps.numpy())
+    np.testing.assert_allclose(p, ref, rtol=1e-5, atol=1e-35)
+    greedy = temps.numpy() == 0
+    assert np.array_equal(p[greedy], logits.float().numpy()[greedy])
+
+
+def tree_case(dev, B, T, V, depth, seed, greedy_frac=0.0, delta=False, same_pq=False,
+              ragged=False, chain=False):
+    rng = np.random.default_rng(seed)
+    g = torch.Generator().manual_seed(seed)
+    P = softmax_rows(g, (B, T, V), 2.0, 0.8)
+    Q = P.clone() if same_pq else softmax_rows(g, (B, T, V), 2.0, 0.8)
+    parents = np.stack([chain_parents(T) if chain else random_tree(T, depth, rng)
+                        for _ in range(B)])
+    # draft tokens drawn from the draft rows of their parents (Gumbel-free inverse CDF)
+    toks = np.zeros((B, T), np.int32)
+    Qn = Q.numpy()
+    for b in range(B):
+        for i in range(1, T):
+            row = Qn[b, parents[b, i]].astype(np.float64)
+            toks[b, i] = min(int(np.searchsorted(np.cumsum(row), rng.random() * row.sum())), V - 1)
+    U = rng.random((B, T)).astype(np.float32)
+    Uf = rng.random(B).astype(np.float32)
+    greedy = rng.random(B) < greedy_frac
+    nn_ = rng.integers(1, T + 1, size=B).astype(np.int32) if ragged else None
+    print(f"[rejection] B={B} T={T} V={V} seed={seed} delta={delta} ragged={ragged}", flush=True)
+    res = rejection_sample_tree(P.to(dev), None if delta else Q.to(dev), torch.from_numpy(toks).to(dev),
+                                torch.from_numpy(parents).to(dev), torch.from_numpy(U).to(dev),
+                                torch.from_numpy(Uf).to(dev), torch.from_numpy(greedy).to(dev),
+                                None if nn_ is None else torch.from_numpy(nn_).to(dev),
+                                "delta" if delta else "stochastic")
+    ref = osamp.rejection_sample_tree(P.numpy(), None if delta else Qn, toks, parents, U, Uf,
+                                      greedy, nn_, delta)
+    names = ("path", "accepted_len", "out_tokens", "next_token")
+    for name, a, r in zip(names, res, ref):
+        assert np.array_equal(a.cpu().numpy(), r), f"{name} differs"
+    return [r for r in ref]
+
+
+@pytest.mark.gpu
+def test_tree_small_vocab_many_cases(dev):
+    for seed in range(6):
+        tree_case(dev, B=16, T=16, V=50, depth=4, seed=seed, greedy_frac=0.25)
+
+
+@pytest.mark.gpu
+def test_tree_delta_mode(dev):
+    for seed in range(3):
+        tree_case(dev, B=16, T=24, V=300, depth=5, seed=100 + seed, delta=True)
+
+
+@pytest.mark.gpu
+def test_tree_ragged_and_odd_vocab(dev):
+    tree_case(dev, B=12, T=20, V=1003, depth=5, seed=7, ragged=True, greedy_frac=0.3)
+
+
+@pytest.mark.gpu
+def test_tree_q_equals_p_accepts_all(dev):
+    path, acc, _, _ = tree_case(dev, B=8, T=9, V=500, depth=8, seed=3, same_pq=True, chain=True)
+    assert (acc == 8).all()
+
+
+@pytest.mark.gpu
+def test_tree64_full_vocab(dev):
+    """Qwen3-8B verify shape at B=16: 64-node depth-8 trees over the full vocabulary."""
+    _, acc, _, _ = tree_case(dev, B=16, T=64, V=V_QWEN, depth=8, seed=11, greedy_frac=0.25)
+    assert acc.min() >= 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("greedy", [False, True])
+def test_chain_config1(dev, greedy):
+    """B=8, k=4, V=151936, logits ~ N(0, 2) softmaxed at T=1 (and a greedy variant)."""
+    B, k, V = 8, 4, V_QWEN
+    g = torch.Generator().manual_seed(1)
+    rng = np.random.default_rng(1)
+    tl = torch.randn(B, k + 1, V, generator=g) * 2
+    dl = torch.randn(B, k, V, generator=g) * 2
+    temps = torch.zeros(B * (k + 1)) if greedy else torch.ones(B * (k + 1))
+    P = temperature_softmax(tl.view(-1, V).to(dev), temps.to(dev)).view(B, k + 1, V)
+    Q = torch.softmax(dl, -1)
+    Qn = Q.numpy()
+    draft = np.zeros((B, k), np.int32)
+    for b in range(B):
+        for i in range(k):
+            c = np.cumsum(Qn[b, i].astype(np.float64))
+            draft[b, i] = min(int(np.searchsorted(c, rng.random() * c[-1])), V - 1)
+    U = rng.random((B, k)).astype(np.float32)
+    Uf = rng.random(B).astype(np.float32)
+    gflag = torch.full((B,), greedy)
+    out = rejection_sample_chain(P, Q.to(dev), torch.from_numpy(draft).to(dev),
+                                 torch.from_numpy(U).to(dev), torch.from_numpy(Uf).to(dev),
+                                 gflag.to(dev))
+    ref = osamp.rejection_sample_chain(P.cpu().numpy(), Qn, draft, U, Uf, gflag.numpy())
+    for a, r in zip(out, ref):
+        assert np.array_equal(a.cpu().numpy(), r)
+
+
+@pytest.mark.gpu
+def test_invalid_draft_tokens_are_rejected(dev):
+    B, T, V = 4, 5, 64
+    g = torch.Generator().manual_seed(5)
+    P = torch.softmax(torch.randn(B, T, V, generator=g), -1)
+    Q = torch.softmax(torch.randn(B, T, V, generator=g), -1)
+    parents = np.tile(chain_parents(T), (B, 1))
+    toks = np.array([[0, -1, 3, 4, 5], [0, V, 1, 2, 3], [0, 1, 2, 3, 4], [0, 99999, -7, 1, 2]],
+                    np.int32)
+    U = np.zeros((B, T), np.float32)
+    Uf = np.full(B, 0.5, np.float32)
+    res = rejection_sample_tree(P.to(dev), Q.to(dev), torch.from_numpy(toks).to(dev),
+                                torch.from_numpy(parents).to(dev), torch.from_numpy(U).to(dev),
+                                torch.from_numpy(Uf).to(dev))
+    ref = osamp.rejection_sample_tree(P.numpy(), Q.numpy(), toks, parents, U, Uf, np.zeros(B, bool))
+    for a, r in zip(res, ref):
+        assert np.array_equal(a.cpu().numpy(), r)
+    assert res[1].cpu().numpy()[[0, 1, 3]].tolist() == [0, 0, 0]
+
+
+@pytest.mark.gpu
+def test_sampler_distribution(dev):
+    """Sampler()(logits, T): empirical frequencies over 200k draws match softmax(l/T)."""
+    V, N = 12, 200_000
+    logits = torch.linspace(-2, 1.5, V).repeat(N, 1)
+    temps = torch.full((N,), 0.7)
+    tok = Sampler()(logits.to(dev), temps.to(dev)).cpu().numpy()
+    p = torch.softmax(logits[0] / 0.7, -1).numpy()
+    counts = np.bincount(tok, minlength=V)
+    chi2 = ((counts - N * p) ** 2 / (N * p)).sum()
+    assert chi2 < 40.0, chi2  # 11 dof: p(chi2 > 40) ~ 3e-5
+    tg = Sampler()(logits[:8].to(dev), torch.zeros(8).to(dev)).cpu().numpy()
+    assert (tg == V - 1).all()
