@@ -1,0 +1,315 @@
+"""Benchmark: Qwen3-8B-shape speculative verify step, tree-64, batch 64, on one MI355X.
+
+One step = one verify step of 64 sequences, each with 2048 cached context tokens
+and a 64-node depth-8 draft tree: the 36-layer target forward over the 4096 tree
+rows (HIP tree attention over the paged KV cache, torch GEMMs), the LM head, the
+temperature-0.8 softmax and tree rejection sampling against resident fp32 draft
+probabilities, compaction of the accepted paths' KV rows in all 36 layers, and
+the read-back of the accepted lengths.  Weights are random-init bf16 of the
+Qwen3-8B architecture; the cached context K/V, trees, draft distributions and
+tokens are synthetic (seeded).  value = verified tokens/s = sum over the timed
+steps of sum_b (accepted_len_b + 1) / elapsed.
+
+Prints one JSON line.  `--gpus N` with N > 1 exits: this build runs on one GPU.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "nano-vllm-x_amd"))
+sys.path.insert(0, ROOT)
+
+METRIC = "verified tokens/s, Qwen3-8B-shape tree-64 verify b=64; sampler HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "tree_attention_verify8b_pmc.txt")
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--tree-nodes", type=int, default=64)
+    ap.add_argument("--tree-depth", type=int, default=8)
+    ap.add_argument("--context", type=int, default=2048)
+    ap.add_argument("--temperature", type=float, default=0.8)
+    ap.add_argument("--model", default="Qwen3-8B")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-seqs", type=int, default=2,
+                    help="sequences in the CPU-baseline sample (0 disables it)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run a 1 GiB device copy (HBM counter calibration)")
+    return ap.parse_args()
+
+
+def read_pmc_traffic():
+    """HBM bytes per attention launch from the committed rocprofv3 --pmc summary."""
+    try:
+        with open(PMC_SUMMARY) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
+def build_step(args, torch, dev):
+    import numpy as np
+    from nanovllm import _C
+    from nanovllm.layers.sampler import RejectionSampler
+    from nanovllm.models.qwen3 import Qwen3ForCausalLM, qwen3_config, random_init_
+    from nanovllm.spec.kv_compact import kv_compact
+    from nanovllm.spec.tree import random_tree
+    from nanovllm.utils.context import set_context, reset_context
+    from nanovllm.utils.synthetic import VerifyBatch
+
+    _C.lib()
+    cfg = qwen3_config(args.model)
+    torch.set_default_dtype(torch.bfloat16)
+    with torch.device(dev):
+        model = Qwen3ForCausalLM(cfg)
+    torch.set_default_dtype(torch.float32)
+    random_init_(model, seed=args.seed)
+    model.eval()
+
+    B, T = args.batch, args.tree_nodes
+    rng = np.random.default_rng(args.seed)
+    trees = [random_tree(T, args.tree_depth, rng) for _ in range(B)]
+    vb = VerifyBatch([args.context] * B, trees, 256, rng)
+    L, Hkv, D = cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim
+    kv_cache = torch.empty(2, L, vb.num_blocks, 256, Hkv, D, dtype=torch.bfloat16, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 1)
+    for i in range(2):
+        for l in range(L):
+            kv_cache[i, l].normal_(0.0, 1.0, generator=gen)
+    for l, attn in enumerate(model.attention_layers()):
+        attn.k_cache, attn.v_cache = kv_cache[0, l], kv_cache[1, l]
+
+    V = cfg.vocab_size
+    # Resident draft distributions (one row per node) and tree tokens drawn from them.
+    Q = torch.empty(B, T, V, dtype=torch.float32, device=dev)
+    for b in range(B):
+        Q[b].normal_(0.0, 2.0, generator=gen)
+        Q[b] = torch.softmax(Q[b] / args.temperature, -1)
+    parents = torch.from_numpy(np.stack(trees)).to(dev)
+    tokens = torch.empty(B, T, dtype=torch.int64, device=dev)
+    tokens[:, 0] = torch.randint(0, V, (B,), generator=gen, device=dev)
+    child = torch.arange(1, T, device=dev)
+    for b in range(B):
+        # node i's token is an independent draw from its parent's draft row
+        drawn = torch.multinomial(Q[b], T, replacement=True, generator=gen)  # [T rows, T draws]
+        tokens[b, 1:] = drawn[parents[b, 1:].long(), child]
+    tokens32 = tokens.to(torch.int32)
+
+    t = lambda a, dt=torch.int32: torch.from_numpy(a).to(device=dev, dtype=dt)
+    input_ids = tokens.view(-1)
+    positions = t(vb.positions, torch.int64)
+    slot_mapping, cu_q = t(vb.slot_mapping), t(vb.cu_q)
+    context_lens, block_tables = t(vb.context_lens), t(vb.bt)
+    tree_mask = t(vb.masks, torch.int64)
+    ctx = t(vb.ctx)
+    temps = torch.full((B,), args.temperature, dtype=torch.float32, device=dev)
+    sampler = RejectionSampler()
+    ugen = torch.Generator(device=dev).manual_seed(args.seed + 2)
+
+    @torch.inference_mode()
+    def step():
+        set_context(False, cu_seqlens_q=cu_q, slot_mapping=slot_mapping, context_lens=context_lens,
+                    block_tables=block_tables, tree_mask=tree_mask, max_seqlen_q=T,
+                    max_context_len=int(vb.context_lens.max()))
+        hidden = model(input_ids, positions)
+        logits = model.compute_logits(hidden)
+        reset_context()
+        U = torch.rand(B, T, device=dev, generator=ugen)
+        Uf = torch.rand(B, device=dev, generator=ugen)
+        path, acc, out_tok, nxt = sampler(logits, temps, Q, tokens32, parents, U, Uf)
+        kv_compact(kv_cache[0], kv_cache[1], block_tables, ctx, path, acc)
+        return acc.cpu()
+
+    state = dict(model=model, kv_cache=kv_cache, vb=vb, Q=Q, tokens=tokens32, parents=parents,
+                 cfg=cfg, temps=temps)
+    return step, state
+
+
+def cpu_baseline(args, torch, state, nseq):
+    """The same verify step restated on the host for a sample of `nseq` sequences:
+    torch-CPU fp32 dense layers plus the oracle's paged tree attention, softmax,
+    rejection sampler and compaction.  Returns (verified tokens/s, cores, seconds)."""
+    import numpy as np
+    from oracle import attention as oatt, kvcache as okv, sampler as osamp
+
+    cores = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(cores)
+    model, vb, cfg = state["model"], state["vb"], state["cfg"]
+    L, Hq, Hkv, D = cfg.num_hidden_layers, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    bs = 256
+    sel = list(range(nseq))
+    rows = np.concatenate([np.arange(vb.cu_q[b], vb.cu_q[b + 1]) for b in sel])
+    # local copy of the selected sequences' pages (all layers), renumbered 0..n-1
+    used = sorted({int(x) for b in sel for x in vb.bt[b] if x >= 0})
+    remap = {old: i for i, old in enumerate(used)}
+    bt = np.array([[remap.get(int(x), -1) for x in vb.bt[b]] for b in sel], np.int32)
+    idx = torch.tensor(used, device=state["kv_cache"].device)
+    kc = state["kv_cache"][0][:, idx].float().cpu().numpy()  # [L, n, bs, Hkv, D]
+    vc = state["kv_cache"][1][:, idx].float().cpu().numpy()
+    W = {n: p.detach().float().cpu() for n, p in model.named_parameters()}
+    ids = state["tokens"].view(-1).cpu()[rows].long()
+    pos = torch.from_numpy(vb.positions[rows]).long()
+    slots = np.concatenate([okv.slot_of(bt[i], vb.ctx[b] + np.arange(vb.qlens[b]), bs)
+                            for i, b in enumerate(sel)])
+    cu = np.zeros(nseq + 1, np.int32)
+    cu[1:] = np.cumsum(vb.qlens[sel])
+    ctxl = vb.context_lens[sel]
+    masks = np.concatenate([vb.masks[vb.cu_q[b]:vb.cu_q[b + 1]] for b in sel]).view(np.uint64)
+    Qs = state["Q"][:nseq].cpu().numpy()
+    par = state["parents"][:nseq].cpu().numpy()
+    toks = state["tokens"][:nseq].cpu().numpy()
+    rng = np.random.default_rng(7)
+    U = rng.random((nseq, vb.T)).astype(np.float32)
+    Uf = rng.random(nseq).astype(np.float32)
+    theta = 1000000.0
+    inv_freq = 1.0 / (theta ** (torch.arange(0, D, 2, dtype=torch.float) / D))
+    freqs = torch.outer(pos.float(), inv_freq)
+    cos, sin = freqs.cos().unsqueeze(1), freqs.sin().unsqueeze(1)
+
+    def rms(x, w, eps=cfg.rms_norm_eps):
+        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w
+
+    def rope(x):
+        x1, x2 = x.chunk(2, -1)
+        return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), -1)
+
+    t0 = time.perf_counter()
+    with torch.inference_mode():
+        h = W["model.embed_tokens.weight"][ids]
+        res = None
+        for l in range(L):
+            pre = f"model.layers.{l}."
+            if res is None:
+                res = h
+            else:
+                res = h + res
+            x = rms(res, W[pre + "input_layernorm.weight"])
+            qkv = x @ W[pre + "self_attn.qkv_proj.weight"].T
+            q, k, v = qkv.split([Hq * D, Hkv * D, Hkv * D], -1)
+            q = rope(rms(q.view(-1, Hq, D), W[pre + "self_attn.q_norm.weight"]))
+            k = rope(rms(k.view(-1, Hkv, D), W[pre + "self_attn.k_norm.weight"]))
+            kl, vl = kc[l], vc[l]
+            okv.store_kvcache(k.numpy(), v.view(-1, Hkv, D).numpy(), kl, vl, slots)
+            o = oatt.paged_attention(q.numpy(), kl, vl, bt, cu, ctxl, masks, D ** -0.5, bs)
+            h = torch.from_numpy(o).view(-1, Hq * D) @ W[pre + "self_attn.o_proj.weight"].T
+            res = h + res
+            x = rms(res, W[pre + "post_attention_layernorm.weight"])
+            gate, up = (x @ W[pre + "mlp.gate_up_proj.weight"].T).chunk(2, -1)
+            h = (torch.nn.functional.silu(gate) * up) @ W[pre + "mlp.down_proj.weight"].T
+        x = rms(h + res, W["model.norm.weight"])
+        logits = (x @ W["lm_head.weight"].T).numpy()
+        P = osamp.temperature_softmax(logits, np.full(len(rows), args.temperature, np.float32))
+        path, acc, _, _ = osamp.rejection_sample_tree(P.reshape(nseq, vb.T, -1), Qs, toks, par, U,
+                                                      Uf, np.zeros(nseq, bool))
+        okv.kv_compact(kc, vc, bt, vb.ctx[sel], path, acc, bs)
+    dt = time.perf_counter() - t0
+    return float((acc + 1).sum()) / dt, cores, dt
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs the verify path on one GPU; --gpus must be 1",
+                          "n_gpus": args.gpus}), flush=True)
+        sys.exit(2)
+    import torch
+    from nanovllm import _C
+
+    dev = torch.device("cuda:0")
+    print(f"[bench] building {args.model} verify step: B={args.batch} T={args.tree_nodes} "
+          f"depth={args.tree_depth} ctx={args.context}", file=sys.stderr, flush=True)
+    step, state = build_step(args, torch, dev)
+    for i in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    print("[bench] warmup done", file=sys.stderr, flush=True)
+
+    _C.timing_reset()
+    _C.timing_enable(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    verified, accepted = 0, 0
+    for i in range(args.steps):
+        acc = step()
+        verified += int((acc + 1).sum())
+        accepted += int(acc.sum())
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    _C.timing_enable(False)
+    timers = {k: _C.timing_read(i) for k, i in (
+        ("tree_attention", _C.TIMER_TREE_ATTENTION), ("softmax", _C.TIMER_SOFTMAX),
+        ("rejection", _C.TIMER_REJECTION), ("kv_compact", _C.TIMER_KV_COMPACT),
+        ("store_kvcache", _C.TIMER_STORE_KV))}
+    print(f"[bench] timed {args.steps} steps in {elapsed:.3f}s", file=sys.stderr, flush=True)
+
+    vb, cfg = state["vb"], state["cfg"]
+    B, T, V = args.batch, args.tree_nodes, cfg.vocab_size
+    Hq, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    avg = lambda k: timers[k][0] / max(timers[k][1], 1)
+    # tree attention, per launch (one layer): K+V of every cached position read once,
+    # q read and o written once.
+    attn_bytes = float(vb.context_lens.sum()) * Hkv * D * 2 * 2 + 2.0 * B * T * Hq * D * 2
+    attn_ms = avg("tree_attention")
+    attn_gbs = attn_bytes / (attn_ms * 1e-3) / 1e9
+    traffic = read_pmc_traffic()
+    smax_bytes = float(B * T) * V * (2 + 4)  # bf16 logits in, fp32 probabilities out
+    smax_ms = avg("softmax")
+    smax_gbs = smax_bytes / (smax_ms * 1e-3) / 1e9
+
+    out = {
+        "metric": METRIC,
+        "value": verified / elapsed,
+        "unit": "verified tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": elapsed / args.steps * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights, seeded context K/V, trees and draft probs)",
+        "config": {"workload": f"{args.model}-shape tree verify step", "batch": B,
+                   "tree_nodes": T, "tree_depth": args.tree_depth, "context": args.context,
+                   "layers": cfg.num_hidden_layers, "hidden": cfg.hidden_size, "q_heads": Hq,
+                   "kv_heads": Hkv, "head_dim": D, "vocab": V, "temperature": args.temperature,
+                   "kv_block": 256},
+        "mean_accepted_per_step": accepted / (args.steps * B),
+        "roofline": {"kernel": "tree_attention", "bound": "hbm", "achieved": attn_gbs,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": attn_gbs / HBM_PEAK_GBS,
+                     "traffic": traffic, "algorithmic_bytes": attn_bytes,
+                     "avg_launch_us": attn_ms * 1e3, "launches": timers["tree_attention"][1]},
+        "sampler": {"softmax_avg_us": smax_ms * 1e3, "softmax_bytes": smax_bytes,
+                    "softmax_GBs": smax_gbs, "softmax_frac": smax_gbs / HBM_PEAK_GBS,
+                    "rejection_avg_us": avg("rejection") * 1e3},
+        "kernels_us_per_step": {k: v[0] / args.steps * 1e3 for k, v in timers.items()},
+    }
+    if args.calib_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+    if args.cpu_seqs > 0:
+        print(f"[bench] cpu baseline on {args.cpu_seqs} sequences", file=sys.stderr, flush=True)
+        v, cores, secs = cpu_baseline(args, torch, state, args.cpu_seqs)
+        out["cpu_baseline"] = {
+            "value": v, "unit": "verified tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{args.cpu_seqs} of {B} sequences ({args.cpu_seqs * T} tree rows) through "
+                      f"the full verify step on the host: torch-CPU fp32 dense layers + oracle "
+                      f"tree attention, softmax, rejection sampling, compaction; {secs:.1f} s"}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,161 @@
+"""Qwen3 decoder (single GPU) calling the verify-path attention layer.
+
+Mirrors the reference's nanovllm/models/qwen3.py:14-216 (module names, fused
+qkv_proj / gate_up_proj, q/k RMSNorm, NeoX RoPE, add+RMSNorm residual stream,
+``compute_logits`` over every row).  Tensor parallelism is left out: one process
+drives one GPU.  Dense projections are torch (hipBLASLt) GEMMs; attention is
+``nanovllm.layers.attention.Attention`` on the HIP library.
+"""
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from nanovllm.layers.attention import Attention
+from nanovllm.layers.layernorm import RMSNorm
+from nanovllm.layers.rotary_embedding import get_rope
+
+
+class Qwen3Attention(nn.Module):
+
+    def __init__(self, hidden_size, num_heads, num_kv_heads, max_position=4096 * 32,
+                 head_dim=None, rms_norm_eps=1e-06, qkv_bias=False, rope_theta=10000,
+                 rope_scaling=None):
+        super().__init__()
+        self.num_heads = num_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim or hidden_size // num_heads
+        self.q_size = self.num_heads * self.head_dim
+        self.kv_size = self.num_kv_heads * self.head_dim
+        self.scaling = self.head_dim ** -0.5
+        self.qkv_bias = qkv_bias
+        self.qkv_proj = nn.Linear(hidden_size, self.q_size + 2 * self.kv_size, bias=qkv_bias)
+        self.o_proj = nn.Linear(self.q_size, hidden_size, bias=False)
+        if isinstance(rope_scaling, dict):
+            rope_theta = rope_scaling.get("rope_theta", rope_theta)
+        self.rotary_emb = get_rope(self.head_dim, self.head_dim, max_position, rope_theta)
+        self.attn = Attention(self.num_heads, self.head_dim, self.scaling, self.num_kv_heads)
+        if not self.qkv_bias:
+            self.q_norm = RMSNorm(self.head_dim, eps=rms_norm_eps)
+            self.k_norm = RMSNorm(self.head_dim, eps=rms_norm_eps)
+
+    def forward(self, positions, hidden_states):
+        qkv = self.qkv_proj(hidden_states)
+        q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
+        q = q.view(-1, self.num_heads, self.head_dim)
+        k = k.view(-1, self.num_kv_heads, self.head_dim)
+        v = v.view(-1, self.num_kv_heads, self.head_dim)
+        if not self.qkv_bias:
+            q = self.q_norm(q)
+            k = self.k_norm(k)
+        q, k = self.rotary_emb(positions, q, k)
+        o = self.attn(q, k, v)
+        return self.o_proj(o.flatten(1, -1))
+
+
+class Qwen3MLP(nn.Module):
+
+    def __init__(self, hidden_size, intermediate_size, hidden_act):
+        super().__init__()
+        assert hidden_act == "silu"
+        self.gate_up_proj = nn.Linear(hidden_size, 2 * intermediate_size, bias=False)
+        self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
+
+    def forward(self, x):
+        gate, up = self.gate_up_proj(x).chunk(2, -1)
+        return self.down_proj(F.silu(gate) * up)
+
+
+class Qwen3DecoderLayer(nn.Module):
+
+    def __init__(self, config):
+        super().__init__()
+        self.self_attn = Qwen3Attention(
+            hidden_size=config.hidden_size,
+            num_heads=config.num_attention_heads,
+            num_kv_heads=config.num_key_value_heads,
+            max_position=config.max_position_embeddings,
+            rms_norm_eps=config.rms_norm_eps,
+            qkv_bias=getattr(config, "attention_bias", False),
+            head_dim=getattr(config, "head_dim", None),
+            rope_theta=getattr(config, "rope_theta", None) or 1000000,
+            rope_scaling=getattr(config, "rope_scaling", None),
+        )
+        self.mlp = Qwen3MLP(config.hidden_size, config.intermediate_size, config.hidden_act)
+        self.input_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+        self.post_attention_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+
+    def forward(self, positions, hidden_states, residual):
+        if residual is None:
+            hidden_states, residual = self.input_layernorm(hidden_states), hidden_states
+        else:
+            hidden_states, residual = self.input_layernorm(hidden_states, residual)
+        hidden_states = self.self_attn(positions, hidden_states)
+        hidden_states, residual = self.post_attention_layernorm(hidden_states, residual)
+        return self.mlp(hidden_states), residual
+
+
+class Qwen3Model(nn.Module):
+
+    def __init__(self, config):
+        super().__init__()
+        self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size)
+        self.layers = nn.ModuleList([Qwen3DecoderLayer(config)
+                                     for _ in range(config.num_hidden_layers)])
+        self.norm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+
+    def forward(self, input_ids, positions):
+        hidden_states = self.embed_tokens(input_ids)
+        residual = None
+        for layer in self.layers:
+            hidden_states, residual = layer(positions, hidden_states, residual)
+        hidden_states, _ = self.norm(hidden_states, residual)
+        return hidden_states
+
+
+class Qwen3ForCausalLM(nn.Module):
+
+    def __init__(self, config):
+        super().__init__()
+        self.model = Qwen3Model(config)
+        self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+        if getattr(config, "tie_word_embeddings", False):
+            self.lm_head.weight = self.model.embed_tokens.weight
+
+    def forward(self, input_ids, positions):
+        return self.model(input_ids, positions)
+
+    def compute_logits(self, hidden_states):
+        return self.lm_head(hidden_states)
+
+    def attention_layers(self):
+        return [m for m in self.modules() if isinstance(m, Attention)]
+
+
+def random_init_(model, std=0.02, seed=0):
+    """Random-init every weight in place (N(0, std); norms at 1)."""
+    gen = torch.Generator(device=next(model.parameters()).device).manual_seed(seed)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if name.endswith("norm.weight"):
+                p.fill_(1.0)
+            else:
+                p.normal_(0.0, std, generator=gen)
+    return model
+
+
+def qwen3_config(name):
+    """Public Qwen3 architecture shapes (no checkpoint needed)."""
+    from transformers import Qwen3Config
+    shapes = {
+        "Qwen3-8B": dict(hidden_size=4096, intermediate_size=12288, num_hidden_layers=36,
+                         num_attention_heads=32, num_key_value_heads=8, head_dim=128,
+                         vocab_size=151936, max_position_embeddings=40960, rope_theta=1000000,
+                         rms_norm_eps=1e-6, tie_word_embeddings=False),
+        "Qwen3-0.6B": dict(hidden_size=1024, intermediate_size=3072, num_hidden_layers=28,
+                           num_attention_heads=16, num_key_value_heads=8, head_dim=128,
+                           vocab_size=151936, max_position_embeddings=40960, rope_theta=1000000,
+                           rms_norm_eps=1e-6, tie_word_embeddings=True),
+    }
+    cfg = Qwen3Config(**shapes[name], hidden_act="silu", attention_bias=False)
+    cfg.dtype = torch.bfloat16
+    return cfg
