@@ -1,0 +1,160 @@
+"""Writes the golden fixtures under tests/golden/ (run from the repo root).
+
+The reference (nano-vllm 0.2.0) has no tests, fixtures or implementation of the
+verify path, so the expected outputs come from independent sources available in
+this container, never from the oracle under test:
+
+* ngram_hf.npz          transformers 5.15 PromptLookupCandidateGenerator.get_candidates
+                        (generation/candidate_generator.py:1076-1096) at batch 1.
+* attention_sdpa.npz    torch.nn.functional.scaled_dot_product_attention (fp64, CPU)
+                        on K/V gathered from a paged cache with an explicit mask.
+* sampler_hand.json     tiny rejection-sampling cases whose outputs were worked out
+                        by hand from Leviathan et al. 2023 Alg. 1 / the tree rule.
+
+Usage: python tests/golden/make_golden.py
+"""
+import json
+import os
+import sys
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, os.path.join(ROOT, "nano-vllm-x_amd"))
+
+
+def hf_prompt_lookup(h, max_ngram, k):
+    from transformers.generation.candidate_generator import PromptLookupCandidateGenerator
+    gen = PromptLookupCandidateGenerator(num_output_tokens=k, max_matching_ngram_size=max_ngram,
+                                         max_length=len(h) + 10 * k + 10)
+    ids = torch.tensor([list(h)], dtype=torch.long)
+    cand, _ = gen.get_candidates(ids)
+    return cand[0, len(h):].tolist()
+
+
+def make_ngram():
+    rng = np.random.default_rng(2024)
+    hists, outs, params = [], [], []
+    for i in range(400):
+        L = int(rng.integers(1, 80))
+        vocab = int(rng.choice([2, 3, 5, 20]))
+        h = rng.integers(0, vocab, size=L).astype(np.int32)
+        if i % 5 == 0 and L > 20:  # planted copy
+            n = int(rng.integers(3, 8))
+            s = int(rng.integers(0, L - 2 * n))
+            h[L - n:] = h[s:s + n]
+        max_ngram = int(rng.integers(1, 5))
+        k = int(rng.integers(1, 8))
+        hists.append(h)
+        outs.append(np.array(hf_prompt_lookup(h, max_ngram, k), np.int32))
+        params.append((max_ngram, k))
+    offs = np.cumsum([0] + [len(h) for h in hists]).astype(np.int64)
+    ooffs = np.cumsum([0] + [len(o) for o in outs]).astype(np.int64)
+    np.savez_compressed(os.path.join(HERE, "ngram_hf.npz"), tokens=np.concatenate(hists),
+                        offsets=offs, params=np.array(params, np.int32),
+                        expected=np.concatenate(outs) if outs else np.zeros(0, np.int32),
+                        expected_offsets=ooffs)
+
+
+def make_attention():
+    from nanovllm.spec.tree import random_tree, ancestor_masks
+    from nanovllm.utils.synthetic import VerifyBatch
+    rng = np.random.default_rng(7)
+    g = torch.Generator().manual_seed(7)
+    trees = [random_tree(9, 3, rng), random_tree(5, 2, rng), random_tree(1, 0, rng)]
+    vb = VerifyBatch([70, 3, 300], trees, 64, rng)
+    Hq, Hkv, D, bs = 4, 2, 16, 64
+    kc = torch.randn(vb.num_blocks, bs, Hkv, D, generator=g, dtype=torch.float64)
+    vc = torch.randn(vb.num_blocks, bs, Hkv, D, generator=g, dtype=torch.float64)
+    N = int(vb.cu_q[-1])
+    q = torch.randn(N, Hq, D, generator=g, dtype=torch.float64)
+    out = torch.zeros(N, Hq, D, dtype=torch.float64)
+    for b in range(vb.B):
+        r0, r1 = int(vb.cu_q[b]), int(vb.cu_q[b + 1])
+        cl = int(vb.context_lens[b])
+        pos = np.arange(cl)
+        slots = vb.bt[b][pos // bs].astype(np.int64) * bs + pos % bs
+        K = kc.view(-1, Hkv, D)[slots]
+        Vv = vc.view(-1, Hkv, D)[slots]
+        base = cl - (r1 - r0)
+        mask = torch.zeros(r1 - r0, cl, dtype=torch.bool)
+        mask[:, :base] = True
+        m = ancestor_masks(vb.parents[b]).view(np.uint64)
+        for i in range(r1 - r0):
+            for j in range(r1 - r0):
+                mask[i, base + j] = bool((int(m[i]) >> j) & 1)
+        G = Hq // Hkv
+        Kh = K.permute(1, 0, 2).repeat_interleave(G, 0)  # [Hq, cl, D]
+        Vh = Vv.permute(1, 0, 2).repeat_interleave(G, 0)
+        qh = q[r0:r1].permute(1, 0, 2)  # [Hq, ql, D]
+        o = torch.nn.functional.scaled_dot_product_attention(qh, Kh, Vh, attn_mask=mask,
+                                                             scale=D ** -0.5)
+        out[r0:r1] = o.permute(1, 0, 2)
+    np.savez_compressed(os.path.join(HERE, "attention_sdpa.npz"), q=q.numpy(), k_cache=kc.numpy(),
+                        v_cache=vc.numpy(), block_tables=vb.bt, cu_seqlens_q=vb.cu_q,
+                        context_lens=vb.context_lens, tree_mask=vb.masks, block_size=bs,
+                        expected=out.numpy())
+
+
+def make_sampler_hand():
+    """Hand-worked cases (V = 4).  p = [.1 .2 .3 .4], q = [.4 .3 .2 .1].
+    Chain, one draft token x:
+      x=0: accept iff U*0.4 <= 0.1 (U <= 0.25).  Residual max(p-q,0) = [0,0,.1,.3],
+           normalised [0, 0, .25, .75]; CDF 0, 0, .25, 1.
+      x=3: q=.1 <= p=.4, always accepted; bonus from P[1].
+    Tree, root with children (x=0, x=1) drawn from q:
+      child 1 (x=0) rejected when U > .25 -> cur1 = [0,0,.25,.75];
+      child 2 (x=1): cur1[1] = 0 -> rejected -> residual max(cur1 - q, 0) = [0,0,.05,.65]
+      normalised [0, 0, 1/14, 13/14]; CDF 0, 0, .0714, 1.
+    Values are exactly representable in binary only approximately; uniforms are kept
+    away from the CDF steps so the expected tokens do not depend on rounding."""
+    p = [0.1, 0.2, 0.3, 0.4]
+    q = [0.4, 0.3, 0.2, 0.1]
+    p1 = [0.7, 0.1, 0.1, 0.1]
+    cases = [
+        # chain, x=0 accepted (U=0.2) -> bonus from p1 with U_final 0.5 -> token 0
+        dict(P=[p, p1], Q=[q, q], tokens=[9, 0], parents=[-1, 0], U=[0, 0.2], Uf=0.5,
+             greedy=False, path=[0, 1], accepted=1, next=0),
+        # chain, x=0 rejected (U=0.3); U_final 0.5 -> residual CDF [0,0,.25,1] -> 3
+        dict(P=[p, p1], Q=[q, q], tokens=[9, 0], parents=[-1, 0], U=[0, 0.3], Uf=0.5,
+             greedy=False, path=[0], accepted=0, next=3),
+        # same with U_final 0.2 -> 2
+        dict(P=[p, p1], Q=[q, q], tokens=[9, 0], parents=[-1, 0], U=[0, 0.3], Uf=0.2,
+             greedy=False, path=[0], accepted=0, next=2),
+        # chain, x=3 always accepted even with U = 0.99; bonus from p1 with U_final .95 -> 3
+        dict(P=[p, p1], Q=[q, q], tokens=[9, 3], parents=[-1, 0], U=[0, 0.99], Uf=0.95,
+             greedy=False, path=[0, 1], accepted=1, next=3),
+        # tree: both children rejected; U_final 0.05 -> 2, U_final 0.5 -> 3
+        dict(P=[p, p1, p1], Q=[q, q, q], tokens=[9, 0, 1], parents=[-1, 0, 0], U=[0, 0.3, 0.0],
+             Uf=0.05, greedy=False, path=[0], accepted=0, next=2),
+        dict(P=[p, p1, p1], Q=[q, q, q], tokens=[9, 0, 1], parents=[-1, 0, 0], U=[0, 0.3, 0.0],
+             Uf=0.5, greedy=False, path=[0], accepted=0, next=3),
+        # tree: second child accepted.  After rejecting x=0, cur1 = [0,0,.25,.75]; child 2
+        # has x=3: U*q[3] = U*.1 <= .75 for any U -> accepted; bonus from its row p1.
+        dict(P=[p, p1, p1], Q=[q, q, q], tokens=[9, 0, 3], parents=[-1, 0, 0], U=[0, 0.9, 0.9],
+             Uf=0.1, greedy=False, path=[0, 2], accepted=1, next=0),
+        # greedy: argmax p = 3; children tokens (1, 3) -> second child accepted; then
+        # argmax p1 = 0 -> no child -> next 0
+        dict(P=[p, p1, p1], Q=[q, q, q], tokens=[9, 1, 3], parents=[-1, 0, 0], U=[0, 0, 0],
+             Uf=0.5, greedy=True, path=[0, 2], accepted=1, next=0),
+        # greedy tie: [.4,.1,.4,.1] -> first max index 0
+        dict(P=[[0.4, 0.1, 0.4, 0.1]], Q=[q], tokens=[9], parents=[-1], U=[0], Uf=0.5,
+             greedy=True, path=[0], accepted=0, next=0),
+        # Q = P: accepted whatever U < 1
+        dict(P=[p, p], Q=[p, p], tokens=[9, 1], parents=[-1, 0], U=[0, 0.999], Uf=0.5,
+             greedy=False, path=[0, 1], accepted=1, next=2),
+        # disjoint support: q on token 0, p[0] = 0 -> rejected; residual = p -> U_final .99 -> 3
+        dict(P=[[0.0, 0.5, 0.25, 0.25], p1], Q=[[1.0, 0, 0, 0], p1], tokens=[9, 0],
+             parents=[-1, 0], U=[0, 0.0], Uf=0.99, greedy=False, path=[0], accepted=0, next=3),
+    ]
+    with open(os.path.join(HERE, "sampler_hand.json"), "w") as f:
+        json.dump(cases, f, indent=1)
+
+
+if __name__ == "__main__":
+    make_ngram()
+    make_attention()
+    make_sampler_hand()
+    print("golden fixtures written to", HERE)

@@ -1,0 +1,64 @@
+"""The C ABI: the library loads, exports every function include/nvx_spec.h
+declares, the ctypes binding covers them, and argument validation fails loudly
+(no kernel is launched by these calls, so they run without a GPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "nvx_spec.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:[\w\*\s]+?)\b(nvx_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declarations_are_bound():
+    from nanovllm import _C
+    names = declared()
+    assert len(names) >= 10
+    assert sorted(_C.EXPORTED) == names
+
+
+def test_library_exports_every_symbol():
+    from nanovllm import _C
+    lib = _C.lib()
+    for name in declared():
+        assert hasattr(lib, name), name
+    assert lib.nvx_version() >= 100
+
+
+def test_validation_errors_are_reported():
+    from nanovllm import _C
+    lib = _C.lib()
+    rc = lib.nvx_ngram_propose(None, None, 1, 1, 9, 5, None, None, None)
+    assert rc == -1 and b"max_ngram" in lib.nvx_last_error()
+    rc = lib.nvx_tree_attention(None, None, None, None, None, 1, None, None, None, 1, 1, 1, 1,
+                                8, 8, 64, 256, 1.0, None, 0, None)
+    assert rc == -1 and b"head_dim" in lib.nvx_last_error()
+    rc = lib.nvx_rejection_sample_tree(None, 0, None, 0, 10, None, None, None, 65, None, None, None,
+                                       0, 1, None, None, None, None, None)
+    assert rc == -1 and b"node_stride" in lib.nvx_last_error()
+    with pytest.raises(RuntimeError, match="kv_compact"):
+        _C.check(lib.nvx_kv_compact(None, None, 0, 1, 24, 256, None, 1, None, None, 9, None, 1, None))
+
+
+def test_workspace_size_plan():
+    from nanovllm import _C
+    lib = _C.lib()
+    # one split per (seq, kv head) when the grid already fills the GPU: no workspace
+    assert lib.nvx_tree_attention_workspace_size(64, 4096, 64, 2112, 32, 8, 128) == 0
+    # few long sequences: split-KV partials (fp32 o + lse per split)
+    ws = lib.nvx_tree_attention_workspace_size(2, 2, 1, 4096, 32, 8, 128)
+    assert ws > 0 and ws % (2 * 32 * 129 * 4) == 0
+    assert lib.nvx_tree_attention_workspace_size(2, 2, 1, 4096, 32, 8, 64) == 0
+
+
+def test_ops_refuse_cpu_tensors():
+    import torch
+    from nanovllm.layers.sampler import temperature_softmax
+    with pytest.raises(RuntimeError, match="GPU only"):
+        temperature_softmax(torch.zeros(2, 8), torch.ones(2))

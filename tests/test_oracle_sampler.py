@@ -1,0 +1,201 @@
+"""Pins the sampler oracle: hand-worked cases, library softmax, exact sums,
+closed forms, distribution guarantees, and transformers' chain sampler."""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sampler as osamp
+
+HAND = os.path.join(os.path.dirname(__file__), "golden", "sampler_hand.json")
+
+
+def test_hand_worked_cases():
+    for i, c in enumerate(json.load(open(HAND))):
+        P = np.array(c["P"], np.float32)[None]
+        Q = np.array(c["Q"], np.float32)[None]
+        T = P.shape[1]
+        path, acc, toks, nxt = osamp.rejection_sample_tree(
+            P, Q, np.array([c["tokens"]], np.int32), np.array([c["parents"]], np.int32),
+            np.array([c["U"]], np.float32), np.array([c["Uf"]], np.float32),
+            np.array([c["greedy"]]))
+        assert path[0, :len(c["path"])].tolist() == c["path"], i
+        assert acc[0] == c["accepted"] and nxt[0] == c["next"], i
+
+
+def test_softmax_matches_torch():
+    g = torch.Generator().manual_seed(0)
+    logits = torch.randn(6, 3001, generator=g) * 2
+    temps = torch.tensor([1.0, 0.8, 0.0, 2.0, 0.5, 0.0])
+    out = osamp.temperature_softmax(logits.numpy(), temps.numpy())
+    ref = torch.softmax(logits.double() / temps.clamp_min(1e-30).double()[:, None], -1).float()
+    sto = temps.numpy() > 0
+    np.testing.assert_allclose(out[sto], ref.numpy()[sto], rtol=2e-6, atol=1e-38)
+    assert np.array_equal(out[~sto], logits.numpy()[~sto])
+
+
+@pytest.mark.parametrize("V", [1, 3, 7, 1024, 4097, 151936])
+def test_canonical_sum_vs_fsum(V):
+    rng = np.random.default_rng(V)
+    row = rng.random(V).astype(np.float32) ** 3
+    s = float(osamp.canonical_sum(row))
+    exact = math.fsum(row.astype(np.float64))
+    assert abs(s - exact) <= 1e-6 * exact + 1e-30
+
+
+def test_canonical_sum_order_is_the_stated_one():
+    """Lane t sums groups t, t+1024, ...; a lane-local cancellation is visible."""
+    V = 8192
+    row = np.zeros(V, np.float32)
+    # lane 0 owns groups 0 and 1024 (elements 0..3, 4096..4099), lane 1 owns 4..7:
+    # lane 0 cancels exactly and lane 1 keeps the 1.0, so the canonical sum is 1;
+    # a left-to-right sum absorbs the 1.0 into 1e8 and returns 0.
+    row[0], row[4096], row[4] = 1e8, -1e8, 1.0
+    assert osamp.canonical_sum(row) == np.float32(1.0)
+    acc = np.float32(0)
+    for x in row:
+        acc = np.float32(acc + x)
+    assert acc == np.float32(0.0)
+
+
+def test_cdf_pick_vs_searchsorted():
+    rng = np.random.default_rng(3)
+    for V in (5, 100, 5000, 151936):
+        row = (rng.random(V) ** 4).astype(np.float32)
+        row[rng.random(V) < 0.3] = 0
+        c64 = np.cumsum(row.astype(np.float64))
+        for u in rng.random(20):
+            t = u * c64[-1]
+            j = int(np.searchsorted(c64, t, side="right"))
+            gap = min(abs(c64[min(j, V - 1)] - t), abs(t - (c64[j - 1] if j > 0 else 0.0)))
+            if gap < 1e-5 * c64[-1]:
+                continue  # too close to a step for fp32 to decide
+            assert osamp.cdf_pick(row, u) == j
+
+
+def test_cdf_pick_never_picks_zero_mass():
+    row = np.array([0, 0, 0.5, 0, 0.5, 0, 0], np.float32)
+    assert osamp.cdf_pick(row, 0.0) == 2
+    assert osamp.cdf_pick(row, np.float32(1 - 2 ** -24)) == 4
+    assert osamp.cdf_pick(row, 0.5) == 4
+
+
+def _tree_case(P, Q, tokens, parents, U, Uf, greedy=False):
+    return osamp.sample_tree_one(np.asarray(P, np.float32), np.asarray(Q, np.float32),
+                                 tokens, parents, np.asarray(U, np.float32), Uf, greedy)
+
+
+def test_q_equals_p_always_accepts():
+    rng = np.random.default_rng(0)
+    for _ in range(50):
+        V, k = 30, 4
+        P = rng.dirichlet(np.ones(V), size=k + 1).astype(np.float32)
+        tok = [0] + [int(rng.choice(V, p=P[i].astype(np.float64) / P[i].astype(np.float64).sum()))
+                     for i in range(k)]
+        path, _ = _tree_case(P, P, tok, list(range(-1, k)), rng.random(k + 1) * 0.999,
+                             float(rng.random()))
+        assert len(path) == k + 1
+
+
+def test_disjoint_support_rejects_and_recovers_p():
+    V, n = 6, 6000
+    p = np.array([0, 0, 0.1, 0.2, 0.3, 0.4], np.float32)
+    q = np.array([0.5, 0.5, 0, 0, 0, 0], np.float32)
+    rng = np.random.default_rng(1)
+    counts = np.zeros(V)
+    for _ in range(n):
+        x = int(rng.integers(2))
+        path, nxt = _tree_case([p, p], [q, q], [0, x], [-1, 0], [0, rng.random()], rng.random())
+        assert path == [0]
+        counts[nxt] += 1
+    chi2 = ((counts[2:] - n * p[2:]) ** 2 / (n * p[2:])).sum()
+    assert chi2 < 25  # 3 dof
+
+
+@pytest.mark.parametrize("n_children", [1, 3])
+def test_first_token_is_target_distributed(n_children):
+    """Speculative sampling leaves the first emitted token distributed as P[root]."""
+    V, n = 5, 20000
+    rng = np.random.default_rng(n_children)
+    p = rng.dirichlet(np.ones(V)).astype(np.float32)
+    q = rng.dirichlet(np.ones(V)).astype(np.float32)
+    leaf = rng.dirichlet(np.ones(V)).astype(np.float32)
+    T = 1 + n_children
+    P = [p] + [leaf] * n_children
+    Q = [q] + [q] * n_children
+    parents = [-1] + [0] * n_children
+    counts = np.zeros(V)
+    qd = q.astype(np.float64) / q.astype(np.float64).sum()
+    for _ in range(n):
+        toks = [0] + list(rng.choice(V, size=n_children, p=qd))
+        path, nxt = _tree_case(P, Q, toks, parents, rng.random(T), rng.random())
+        first = toks[path[1]] if len(path) > 1 else nxt
+        counts[first] += 1
+    chi2 = ((counts - n * p) ** 2 / (n * p)).sum()
+    assert chi2 < 25, (counts / n, p)  # 4 dof: p(chi2 > 25) ~ 5e-5
+
+
+def test_chain_acceptance_matches_transformers():
+    """Acceptance counts and first tokens agree in distribution with transformers'
+    _speculative_sampling (generation/utils.py:3992) on the same chain."""
+    from transformers.generation.utils import _speculative_sampling
+    V, k, n = 6, 2, 4000
+    rng = np.random.default_rng(2)
+    tl = torch.from_numpy(rng.normal(size=(k + 1, V)).astype(np.float32))
+    dl = torch.from_numpy(rng.normal(size=(k, V)).astype(np.float32))
+    P = torch.softmax(tl, -1).numpy()
+    Q = torch.softmax(dl, -1).numpy()
+    torch.manual_seed(0)
+    hf = np.zeros(k + 1)
+    ours = np.zeros(k + 1)
+    hf_first, ours_first = np.zeros(V), np.zeros(V)
+    for _ in range(n):
+        draft = [int(rng.choice(V, p=Q[i].astype(np.float64) / Q[i].astype(np.float64).sum()))
+                 for i in range(k)]
+        cand = torch.tensor([[0] + draft])
+        valid, n_match = _speculative_sampling(cand, dl[None], k, tl[None], False)
+        hf[int(n_match)] += 1
+        hf_first[int(valid[0, 0])] += 1
+        toks = [0] + draft
+        path, nxt = _tree_case(P, np.concatenate([Q, Q[:1]]), toks, list(range(-1, k)),
+                               rng.random(k + 1), rng.random())
+        ours[len(path) - 1] += 1
+        ours_first[toks[path[1]] if len(path) > 1 else nxt] += 1
+    tot = hf_first + ours_first
+    m = tot > 0
+    e = tot / 2
+    assert (((hf_first - e) ** 2 / e)[m] + ((ours_first - e) ** 2 / e)[m]).sum() < 25
+    # two-sample chi-square over acceptance counts
+    tot = hf + ours
+    exp_h, exp_o = tot * hf.sum() / tot.sum(), tot * ours.sum() / tot.sum()
+    m = tot > 0
+    chi2 = (((hf - exp_h) ** 2 / exp_h)[m] + ((ours - exp_o) ** 2 / exp_o)[m]).sum()
+    assert chi2 < 20, (hf, ours)
+    # and both match the closed form P(accept first) = sum min(p, q)
+    a1 = np.minimum(P[0], Q[0]).sum()
+    assert abs((n - ours[0]) / n - a1) < 0.03 and abs((n - hf[0]) / n - a1) < 0.03
+
+
+def test_greedy_rule():
+    P = np.array([[0.1, 0.5, 0.4], [0.3, 0.3, 0.4], [0.9, 0.05, 0.05]], np.float32)
+    path, nxt = _tree_case(P, P, [0, 1, 2], [-1, 0, 1], [0, 0, 0], 0.5, greedy=True)
+    assert path == [0, 1, 2] and nxt == 0
+    path, nxt = _tree_case(P, P, [0, 2, 1], [-1, 0, 0], [0, 0, 0], 0.5, greedy=True)
+    assert path == [0, 2] and nxt == 0
+
+
+def test_chain_wrapper_shapes():
+    rng = np.random.default_rng(4)
+    B, k, V = 3, 4, 50
+    P = rng.dirichlet(np.ones(V), size=(B, k + 1)).astype(np.float32)
+    Q = rng.dirichlet(np.ones(V), size=(B, k)).astype(np.float32)
+    d = rng.integers(0, V, size=(B, k)).astype(np.int32)
+    acc, rec, bonus, toks = osamp.rejection_sample_chain(P, Q, d, rng.random((B, k)),
+                                                         rng.random(B), np.zeros(B, bool))
+    for b in range(B):
+        a = acc[b]
+        assert toks[b, :a].tolist() == d[b, :a].tolist()
+        assert (rec[b] == -1) == (a == k) and (bonus[b] == -1) == (a < k)
