@@ -5,13 +5,16 @@
 // nodes (row r -> node r / G, head hk*G + r % G), so one staged K/V chunk serves
 // the whole GQA group.  Each wave owns 32 q rows.
 //
-// Per 64-key chunk the workgroup stages K (row-major) and V (transposed) in LDS,
-// then every wave computes S^T = K . Q^T with v_mfma_f32_32x32x16_bf16: lane l then
-// holds query row l%32 and 16 keys per 32-key tile, so the online-softmax row max
-// and row sum are in-lane plus one exchange with lane l^32.  P^T goes straight from
-// those registers into the B operand of O^T += V^T . P^T (the contraction slots are
-// relabelled to the keys the lane already holds; V^T is read with two 8-byte LDS
-// reads per MFMA).  Global loads of chunk c+1 are issued before computing chunk c.
+// Per 64-key chunk the workgroup stages K and V row-major in LDS (plain 128-bit
+// stores).  Every wave computes S^T = K . Q^T with v_mfma_f32_32x32x16_bf16: lane l
+// then holds query row l%32 and 16 keys per 32-key tile, so the online-softmax row
+// max and row sum are in-lane plus one exchange with lane l^32.  P^T goes straight
+// from those registers into the B operand of O^T += V^T . P^T; the contraction slots
+// are relabelled to the keys the lane already holds, and the V^T A operand comes
+// from two ds_read_b64_tr_b16 (gfx950 LDS transpose reads) per MFMA.
+//
+// Pipeline: two register stages of global loads (chunks c+1 and c+2 in flight while
+// chunk c is computed) and two LDS buffers, one barrier per chunk.
 //
 // Masking: keys < context_len - q_len are visible to all rows; key base+m is
 // visible to node i iff bit m of its tree mask (or m <= i without a mask).
@@ -22,14 +25,18 @@
 namespace {
 
 constexpr int kD = 128;
-constexpr int kKC = 64;            // keys per staged chunk
-constexpr int kKStride = kD + 8;   // bf16 per K row in LDS (272 B: 16-B aligned, bank-skewed)
-constexpr int kVStride = kKC + 8;  // bf16 per V^T row in LDS (144 B)
+constexpr int kKC = 64;                         // keys per staged chunk
+constexpr int kStages = 3;                      // LDS ring: chunk c computed, c+1 and c+2 in flight
+constexpr int kTileBytes = kKC * kD * 2;        // one K (or V) chunk: 64 rows x 256 B
+constexpr int kStageBytes = 2 * kTileBytes;     // K then V
+constexpr int kDmaPerChunk = kStageBytes / 1024;  // 1 KB per wave-wide 16-byte-per-lane load
 constexpr int kTargetWaves = 256 * 16;
+constexpr int kMaxSplitPages = 512;             // block-table entries one KV split may touch
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 
 struct AttnParams {
   const uint16_t* q;
@@ -52,6 +59,28 @@ __device__ __forceinline__ uint16_t f2bf(float x) {
   return (uint16_t)(u >> 16);
 }
 
+// LDS rows are 256 B with no padding; the 16-byte slot of logical segment `seg` in
+// row `row` is seg ^ swz(row).  swz is a bijection on row % 16 (K reads of 16
+// consecutive rows hit 16 different slots) and varies in bits 2-3 over any 4
+// consecutive rows (the 4 rows x 4 segments of a transpose read cover 16 slots),
+// so both read patterns are bank-conflict free.
+__device__ __forceinline__ int swz(int row) { return ((row & 3) << 2) | ((row >> 2) & 3); }
+
+// Wave-wide 16-byte-per-lane load from global memory straight into LDS: lane i's
+// data lands at LDS byte address lds_base + 16*i.  Issued from inline asm so the
+// compiler does not fence every LDS read behind it; completion is waited for
+// explicitly with wait_vm below (each call counts one vector-memory op per wave).
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(gptr), "s"(lds_base)
+               : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
 __device__ __forceinline__ int remap_xcd(int phys, int n) {
   // Blocks are dispatched round-robin over the 8 XCDs; give each XCD a
   // contiguous range of logical ids so the blocks of one (seq, kv head), which
@@ -65,9 +94,9 @@ __device__ __forceinline__ int remap_xcd(int phys, int n) {
 template <int W>
 __global__ __launch_bounds__(W * 64) void tree_attn_kernel(AttnParams p) {
   constexpr int NT = W * 64;
-  constexpr int SEGS = (kKC * kD / 8) / NT;  // 16-byte K (and V) pieces per thread per chunk
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[kKC * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kD * kVStride];
+  constexpr int PER = kDmaPerChunk / W;  // LDS-DMA loads per wave per chunk
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[kStages * kStageBytes];
+  __shared__ int32_t pages[kMaxSplitPages];
 
   const int logical = remap_xcd(blockIdx.x, gridDim.x);
   const int split = logical % p.nsplit;
@@ -86,7 +115,8 @@ __global__ __launch_bounds__(W * 64) void tree_attn_kernel(AttnParams p) {
   if (row0 >= rows_total || qlen <= 0) return;  // uniform over the block
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, g = lane >> 5, lr = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, g = lane >> 5, lr = lane & 31;
   const int r = row0 + wave * 32 + lr;
   const bool row_ok = r < rows_total;
   const int node = row_ok ? r / p.G : 0;
@@ -118,38 +148,41 @@ __global__ __launch_bounds__(W * 64) void tree_attn_kernel(AttnParams p) {
 
   const int32_t* bt = p.block_tables + (int64_t)b * p.bt_stride;
   const int bs = p.block_size;
+  const uint32_t ring_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)ring;
 
-  uint4 kreg[SEGS], vreg[SEGS];
-  auto load_chunk = [&](int c) {
+  // This split's block-table entries go to LDS once, so the loop reads page ids
+  // without touching the vector-memory counter the DMA pipeline waits on.
+  const int page0 = (c0 * kKC) / bs;
+  const int npages = c1 > c0 ? ((c1 * kKC - 1) / bs - page0 + 1) : 0;
+  for (int i = tid; i < npages; i += NT)
+    pages[i] = (page0 + i < p.bt_stride) ? bt[page0 + i] : -1;
+  // Make every prologue global load (Q, mask, pages) complete here, before the
+  // first LDS-DMA is queued behind them.
 #pragma unroll
-    for (int i = 0; i < SEGS; ++i) {
-      const int sid = tid + i * NT;
-      const int key = sid >> 4, seg = sid & 15;
-      const int pos = c * kKC + key;
-      kreg[i] = make_uint4(0, 0, 0, 0);
-      vreg[i] = make_uint4(0, 0, 0, 0);
-      if (pos < ctxlen && pos / bs < p.bt_stride) {
-        const int32_t blk = bt[pos / bs];
-        if (blk >= 0) {
-          const int64_t off = (((int64_t)blk * bs + pos % bs) * p.Hkv + hk) * kD + seg * 8;
-          kreg[i] = *reinterpret_cast<const uint4*>(p.k_cache + off);
-          vreg[i] = *reinterpret_cast<const uint4*>(p.v_cache + off);
-        }
-      }
-    }
-  };
-  auto store_chunk = [&]() {
+  for (int s = 0; s < 8; ++s) asm volatile("" : : "v"(bq[s]));
+  asm volatile("" : : "v"(mbits));
+  __syncthreads();
+
+  // Issue the PER LDS-DMA loads of this wave for chunk c into stage st.  Load
+  // j of wave w fills 4 rows (1 KB) of the K (first 16 loads) or V (last 16)
+  // tile; lane i fetches row 4*(ii%16) + i/16, logical segment (i%16)^swz(row),
+  // so the tile lands swizzled.  Rows at or beyond context_len re-read the chunk's
+  // first row (finite data; their scores are masked to -inf).
+  auto issue_chunk = [&](int c, int st) {
+    const int pos0 = c * kKC;
+    const int32_t blk = pages[pos0 / bs - page0];
+    const int64_t rowbase = blk >= 0 ? (int64_t)blk * bs + pos0 % bs : -1;
 #pragma unroll
-    for (int i = 0; i < SEGS; ++i) {
-      const int sid = tid + i * NT;
-      const int key = sid >> 4, seg = sid & 15;
-      *reinterpret_cast<uint4*>(&k_lds[key * kKStride + seg * 8]) = kreg[i];
-      const uint32_t w[4] = {vreg[i].x, vreg[i].y, vreg[i].z, vreg[i].w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        vt_lds[(seg * 8 + 2 * j) * kVStride + key] = (uint16_t)(w[j] & 0xffffu);
-        vt_lds[(seg * 8 + 2 * j + 1) * kVStride + key] = (uint16_t)(w[j] >> 16);
-      }
+    for (int j = 0; j < PER; ++j) {
+      const int ii = wave + W * j;
+      const int isv = ii >> 4;
+      const int row = 4 * (ii & 15) + (lane >> 4);
+      const int seg = (lane & 15) ^ swz(row);
+      const int rr = (pos0 + row < ctxlen) ? row : 0;
+      const int64_t off =
+          rowbase >= 0 ? ((rowbase + rr) * p.Hkv + hk) * kD + seg * 8 : 0;
+      const uint16_t* src = (isv ? p.v_cache : p.k_cache) + off;
+      dma16(src, ring_base + st * kStageBytes + isv * kTileBytes + (ii & 15) * 1024);
     }
   };
 
@@ -160,24 +193,26 @@ __global__ __launch_bounds__(W * 64) void tree_attn_kernel(AttnParams p) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) oacc[dt][j] = 0.f;
 
-  if (c0 < c1) load_chunk(c0);
-  for (int c = c0; c < c1; ++c) {
-    __syncthreads();
-    store_chunk();
-    __syncthreads();
-    if (c + 1 < c1) load_chunk(c + 1);
-    if (!wave_active) continue;
+  // V^T operand addressing for the transpose reads: 16-lane group q = lane/16
+  // supplies rows (keys) 4*(q/2) + i/4 and d columns 16*(q%2) + 4*(i%4).
+  const int tq = lane >> 4, ti = lane & 15;
+  const int tr_key = 4 * (tq >> 1) + (ti >> 2);
+  const int tr_d = 16 * (tq & 1) + 4 * (ti & 3);
 
+  auto compute_chunk = [&](int st, int c) {
+    const uint16_t* kb = reinterpret_cast<const uint16_t*>(ring + st * kStageBytes);
+    const uint16_t* vb = reinterpret_cast<const uint16_t*>(ring + st * kStageBytes + kTileBytes);
     // S^T tiles: keys kt*32 + (j/4)*8 + 4*g + j%4, query row lr.
     f32x16 sacc[2];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
+      const int krow = kt * 32 + lr;
 #pragma unroll
       for (int j = 0; j < 16; ++j) sacc[kt][j] = 0.f;
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        const bf16x8 a =
-            *reinterpret_cast<const bf16x8*>(&k_lds[(kt * 32 + lr) * kKStride + 16 * s + 8 * g]);
+        const int slot = (2 * s + g) ^ swz(krow);
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&kb[krow * kD + slot * 8]);
         sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq[s], sacc[kt], 0, 0, 0);
       }
     }
@@ -205,23 +240,25 @@ __global__ __launch_bounds__(W * 64) void tree_attn_kernel(AttnParams p) {
     mloc = fmaxf(mloc, nvx::shfl_xor_f(mloc, 32));
     const float m_new = fmaxf(m_run, mloc);
     const bool dead = (m_new == -INFINITY);
-    const float alpha = dead ? 1.f : exp2f(m_run - m_new);
+    const float alpha = dead ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
     float lsum = 0.f;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const float pv = dead ? 0.f : exp2f(sacc[kt][j] - m_new);
+        const float pv = dead ? 0.f : __builtin_amdgcn_exp2f(sacc[kt][j] - m_new);
         sacc[kt][j] = pv;
         lsum += pv;
       }
     lsum += nvx::shfl_xor_f(lsum, 32);
     l_run = l_run * alpha + lsum;
     m_run = m_new;
+    if (__any(alpha != 1.f)) {  // the running max rarely moves after the first chunks
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+      for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
+        for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
+    }
 
     // P^T as B operand: slot (g, i) of k-step ks holds key 16*ks + (i/4)*8 + 4*g + i%4.
     bf16x8 bp[4];
@@ -232,15 +269,35 @@ __global__ __launch_bounds__(W * 64) void tree_attn_kernel(AttnParams p) {
 
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
-      const uint16_t* vrow = &vt_lds[(dt * 32 + lr) * kVStride + 4 * g];
+      const int d = dt * 32 + tr_d;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vrow + 16 * ks);
-        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vrow + 16 * ks + 8);
+        const int r0 = 16 * ks + tr_key, r1 = r0 + 8;
+        const uint16_t* a0 = &vb[r0 * kD + (((d >> 3) ^ swz(r0)) << 3) + (d & 7)];
+        const uint16_t* a1 = &vb[r1 * kD + (((d >> 3) ^ swz(r1)) << 3) + (d & 7)];
+        const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(a0));
+        const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(a1));
         const bf16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bp[ks], oacc[dt], 0, 0, 0);
       }
     }
+  };
+
+  // Ring pipeline, one barrier per chunk: wait for chunk c's loads (chunk c+1's may
+  // still be in flight), barrier (also: every wave is done with chunk c-1, whose
+  // stage receives chunk c+2), issue chunk c+2, compute chunk c.
+  if (c0 < c1) issue_chunk(c0, 0);
+  if (c0 + 1 < c1) issue_chunk(c0 + 1, 1);
+  int st = 0;
+  for (int c = c0; c < c1; ++c) {
+    if (c + 1 < c1)
+      wait_vm<PER>();
+    else
+      wait_vm<0>();
+    __syncthreads();
+    if (c + 2 < c1) issue_chunk(c + 2, st == 0 ? 2 : st - 1);
+    if (wave_active) compute_chunk(st, c);
+    st = st == kStages - 1 ? 0 : st + 1;
   }
 
   if (!row_ok || token >= p.total_q) return;
@@ -301,8 +358,8 @@ struct Plan {
 Plan make_plan(int num_seqs, int max_q, int max_ctx, int Hq, int Hkv) {
   const int G = Hq / Hkv;
   const int rows = G * (max_q > 0 ? max_q : 1);
-  int W = 1;
-  while (W < 8 && W * 32 < rows) W *= 2;
+  // 4 or 8 waves: enough threads to keep two chunks of K/V loads in flight.
+  const int W = rows <= 128 ? 4 : 8;
   Plan pl;
   pl.W = W;
   pl.nq = (rows + W * 32 - 1) / (W * 32);
@@ -359,6 +416,13 @@ extern "C" int nvx_tree_attention(const void* q, void* o, const void* k_cache, c
   NVX_CHECK(q && o && k_cache && v_cache && block_tables && cu_seqlens_q && context_lens,
             "tree_attention: null pointer");
   const Plan pl = make_plan(num_seqs, max_seqlen_q, max_context_len, num_heads, num_kv_heads);
+  {
+    const int chunks = (max_context_len + kKC - 1) / kKC;
+    const int cps = (chunks + pl.nsplit - 1) / pl.nsplit;
+    NVX_CHECK((cps * kKC + block_size - 1) / block_size + 1 <= kMaxSplitPages,
+              "tree_attention: context of %d tokens spans more than %d pages per split",
+              max_context_len, kMaxSplitPages);
+  }
   const size_t need = workspace_bytes_for(pl, total_q, num_heads);
   NVX_CHECK(workspace_bytes >= need && (need == 0 || workspace != nullptr),
             "tree_attention: workspace of %zu bytes required (got %zu)", need, workspace_bytes);
@@ -390,12 +454,10 @@ extern "C" int nvx_tree_attention(const void* q, void* o, const void* k_cache, c
   const int64_t nblocks = (int64_t)num_seqs * num_kv_heads * pl.nq * pl.nsplit;
   NVX_CHECK(nblocks < (1ll << 31), "tree_attention: grid too large");
   const dim3 grid((unsigned)nblocks);
-  switch (pl.W) {
-    case 1: hipLaunchKernelGGL(tree_attn_kernel<1>, grid, dim3(64), 0, s, p); break;
-    case 2: hipLaunchKernelGGL(tree_attn_kernel<2>, grid, dim3(128), 0, s, p); break;
-    case 4: hipLaunchKernelGGL(tree_attn_kernel<4>, grid, dim3(256), 0, s, p); break;
-    default: hipLaunchKernelGGL(tree_attn_kernel<8>, grid, dim3(512), 0, s, p); break;
-  }
+  if (pl.W == 4)
+    hipLaunchKernelGGL(tree_attn_kernel<4>, grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(tree_attn_kernel<8>, grid, dim3(512), 0, s, p);
   NVX_LAUNCHED();
   if (pl.nsplit > 1) {
     hipLaunchKernelGGL(combine_kernel, dim3(total_q * num_heads), dim3(kD), 0, s, p.part_o,
