@@ -70,10 +70,10 @@ __device__ __forceinline__ int swz(int row) { return ((row & 3) << 2) | ((row >>
 // data lands at LDS byte address lds_base + 16*i.  Issued from inline asm so the
 // compiler does not fence every LDS read behind it; completion is waited for
 // explicitly with wait_vm below (each call counts one vector-memory op per wave).
-__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
                :
-               : "v"(gptr), "s"(lds_base)
+               : "v"(voff), "s"(sbase), "s"(lds_base)
                : "memory", "m0");
 }
 template <int N>
@@ -166,23 +166,34 @@ __global__ __launch_bounds__(W * 64) void tree_attn_kernel(AttnParams p) {
   // Issue the PER LDS-DMA loads of this wave for chunk c into stage st.  Load
   // j of wave w fills 4 rows (1 KB) of the K (first 16 loads) or V (last 16)
   // tile; lane i fetches row 4*(ii%16) + i/16, logical segment (i%16)^swz(row),
-  // so the tile lands swizzled.  Rows at or beyond context_len re-read the chunk's
-  // first row (finite data; their scores are masked to -inf).
+  // so the tile lands swizzled.  The per-lane byte offset within a chunk is loop
+  // invariant; the chunk's page start is a scalar base.  In a chunk that ends
+  // past context_len the missing rows re-read the chunk's first row (finite data;
+  // their scores are masked to -inf).
+  const int row_stride = p.Hkv * kD * 2;  // bytes between consecutive tokens
+  uint32_t lane_off[PER];
+  int lane_row[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int ii = wave + W * j;
+    const int row = 4 * (ii & 15) + (lane >> 4);
+    const int seg = (lane & 15) ^ swz(row);
+    lane_row[j] = row;
+    lane_off[j] = (uint32_t)(hk * kD * 2 + seg * 16);
+  }
   auto issue_chunk = [&](int c, int st) {
     const int pos0 = c * kKC;
     const int32_t blk = pages[pos0 / bs - page0];
-    const int64_t rowbase = blk >= 0 ? (int64_t)blk * bs + pos0 % bs : -1;
+    const int64_t tok0 = blk >= 0 ? (int64_t)blk * bs + pos0 % bs : 0;
+    const char* kbase = reinterpret_cast<const char*>(p.k_cache) + tok0 * row_stride;
+    const char* vbase = reinterpret_cast<const char*>(p.v_cache) + tok0 * row_stride;
+    const bool full = pos0 + kKC <= ctxlen;
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int ii = wave + W * j;
-      const int isv = ii >> 4;
-      const int row = 4 * (ii & 15) + (lane >> 4);
-      const int seg = (lane & 15) ^ swz(row);
-      const int rr = (pos0 + row < ctxlen) ? row : 0;
-      const int64_t off =
-          rowbase >= 0 ? ((rowbase + rr) * p.Hkv + hk) * kD + seg * 8 : 0;
-      const uint16_t* src = (isv ? p.v_cache : p.k_cache) + off;
-      dma16(src, ring_base + st * kStageBytes + isv * kTileBytes + (ii & 15) * 1024);
+      const int row = full || pos0 + lane_row[j] < ctxlen ? lane_row[j] : 0;
+      dma16(ii >> 4 ? vbase : kbase, lane_off[j] + (uint32_t)(row * row_stride),
+            ring_base + st * kStageBytes + (ii >> 4) * kTileBytes + (ii & 15) * 1024);
     }
   };
 
@@ -216,14 +227,16 @@ __global__ __launch_bounds__(W * 64) void tree_attn_kernel(AttnParams p) {
         sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq[s], sacc[kt], 0, 0, 0);
       }
     }
+    // Mask, then take the row max.  Scores stay unscaled; the scale (times
+    // log2 e) is folded into the exponent below.
     const int pos0 = c * kKC;
-    const bool need_mask = pos0 + kKC > base;
+    const bool need_mask = pos0 + kKC > base;  // tree keys or keys past context_len
     float mloc = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        float sv = sacc[kt][j] * p.scale_log2;
+        float sv = sacc[kt][j];
         if (need_mask) {
           const int key = pos0 + kt * 32 + (j >> 2) * 8 + 4 * g + (j & 3);
           bool vis = key < ctxlen;
@@ -237,28 +250,33 @@ __global__ __launch_bounds__(W * 64) void tree_attn_kernel(AttnParams p) {
         mloc = fmaxf(mloc, sv);
       }
     }
-    mloc = fmaxf(mloc, nvx::shfl_xor_f(mloc, 32));
-    const float m_new = fmaxf(m_run, mloc);
-    const bool dead = (m_new == -INFINITY);
-    const float alpha = dead ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+    mloc = fmaxf(mloc, nvx::shfl_xor_f(mloc, 32)) * p.scale_log2;
+    // The reference max only moves up when a row's max grows by more than 2^8:
+    // P then stays <= 256 (exact after the final 1/l), and the O rescale is rare.
+    const bool grow = mloc > m_run + 8.f;
+    if (__any(grow)) {
+      const float m_new = grow ? mloc : m_run;
+      const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
+      m_run = m_new;
+    }
+    const bool dead = (m_run == -INFINITY);
+    const float neg_m = dead ? 0.f : -m_run;
     float lsum = 0.f;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const float pv = dead ? 0.f : __builtin_amdgcn_exp2f(sacc[kt][j] - m_new);
+        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][j], p.scale_log2, neg_m));
         sacc[kt][j] = pv;
         lsum += pv;
       }
     lsum += nvx::shfl_xor_f(lsum, 32);
-    l_run = l_run * alpha + lsum;
-    m_run = m_new;
-    if (__any(alpha != 1.f)) {  // the running max rarely moves after the first chunks
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
-    }
+    l_run += lsum;
 
     // P^T as B operand: slot (g, i) of k-step ks holds key 16*ks + (i/4)*8 + 4*g + i%4.
     bf16x8 bp[4];
