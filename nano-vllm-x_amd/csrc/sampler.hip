@@ -1,16 +1,15 @@
 // Sampler kernels: temperature softmax and tree / chain rejection sampling.
 //
-// temperature_softmax: one workgroup (1024 threads) per row.  For bf16 rows of up
-//   to 1024*8*kRegChunks elements the row is loaded once into registers with
-//   128-bit loads (row max, sum of exp, then the fp32 write come from registers);
-//   other rows stream twice (online max/sum, then write).  HBM bound: it reads the
-//   logits once and writes fp32 probabilities once.
+// temperature_softmax: one workgroup per row, two streaming passes (online max and
+//   sum, then the fp32 write); 128-bit accesses when rows are 16-byte aligned.  HBM
+//   bound: logits read (the second pass mostly from the Infinity Cache) and fp32
+//   probabilities written once.
 //
 // rejection_sample_tree: one workgroup (1024 threads) per sequence walks the draft
 //   tree from the root.  Per visited node the acceptance tests need two scalars;
-//   each rejection needs one pass over the node's target/draft rows to normalise
-//   the residual, and the final draw one inverse-CDF pass.  Only rows on the walk
-//   are read.  The fp32 association order of every sum and scan is fixed (see
+//   in stochastic mode each rejection needs one pass over the node's target/draft
+//   rows to renormalise the residual (delta mode updates a scalar), and the final
+//   draw one inverse-CDF pass.  Only rows on the walk are read.  The fp32 association order of every sum and scan is fixed (see
 //   nvx_internal.h) so integer outputs are reproducible bit for bit by the CPU
 //   restatement given the same probabilities and uniforms.
 #include <float.h>
@@ -23,7 +22,6 @@ namespace {
 
 constexpr int kNT = 1024;
 constexpr int kNW = kNT / nvx::kWave;
-constexpr int kRegChunks = 19;  // 16-byte chunks per thread: V <= 155648 bf16
 constexpr int kMaxNodes = 64;
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
@@ -35,71 +33,131 @@ __device__ __forceinline__ float load_logit(const void* row, int i, int dtype) {
   return __uint_as_float((uint32_t)h << 16);
 }
 
-// ------------------------------------------------------------ softmax (regs)
-__global__ __launch_bounds__(kNT) void softmax_bf16_regs_kernel(const uint16_t* __restrict__ logits,
-                                                                int64_t stride,
-                                                                const float* __restrict__ temps,
-                                                                float* __restrict__ probs, int V) {
-  __shared__ float red[kNW];
+// ------------------------------------------------------- softmax (vectorised)
+// One 1024-thread workgroup per row, two streaming passes over the logits: online
+// max / sum in log2 units (x * log2(e) / T) with four 16-byte loads in flight per
+// thread, then exp2(fma(x, log2(e)/T, -max)) * (1/sum) written as 128-bit stores.
+// With at most two rows per CU in flight (~150 MB of rows GPU-wide) the second
+// read of a row is served by the Infinity Cache.  1/T folded into the FMA
+// keeps the relative error ~1e-6 (contract tolerance 1e-5).
+constexpr int kVecNT = 1024;
+constexpr int kUnroll = 4;
+
+template <typename VT>
+struct VecTraits;
+template <>
+struct VecTraits<uint16_t> {  // bf16: 8 values per 16 bytes
+  static constexpr int kPer = 8;
+  __device__ static void expand(const uint4& w, float (&x)[8]) {
+    x[0] = bf16_lo(w.x); x[1] = bf16_hi(w.x); x[2] = bf16_lo(w.y); x[3] = bf16_hi(w.y);
+    x[4] = bf16_lo(w.z); x[5] = bf16_hi(w.z); x[6] = bf16_lo(w.w); x[7] = bf16_hi(w.w);
+  }
+};
+template <>
+struct VecTraits<float> {  // fp32: 4 values per 16 bytes
+  static constexpr int kPer = 4;
+  __device__ static void expand(const uint4& w, float (&x)[4]) {
+    x[0] = __uint_as_float(w.x); x[1] = __uint_as_float(w.y);
+    x[2] = __uint_as_float(w.z); x[3] = __uint_as_float(w.w);
+  }
+};
+
+template <typename VT>
+__global__ __launch_bounds__(kVecNT) void softmax_vec_kernel(const VT* __restrict__ logits,
+                                                             int64_t stride,
+                                                             const float* __restrict__ temps,
+                                                             float* __restrict__ probs, int V) {
+  using Tr = VecTraits<VT>;
+  constexpr int P = Tr::kPer;
+  __shared__ float red[kVecNT / nvx::kWave];
   const int row = blockIdx.x;
   const float T = temps[row];
-  const bool greedy = (T == 0.f);
   const uint4* src = reinterpret_cast<const uint4*>(logits + (int64_t)row * stride);
-  float4* dst = reinterpret_cast<float4*>(probs + (int64_t)row * V);
-  const int nvec = V / 8;
-
-  uint4 buf[kRegChunks];
+  float* dst = probs + (int64_t)row * V;
+  const int nvec = V / P;
+  const int tid = threadIdx.x;
+  if (T == 0.f) {  // greedy row: fp32 logits unchanged
+    for (int i = tid; i < nvec; i += kVecNT) {
+      float x[P];
+      Tr::expand(src[i], x);
 #pragma unroll
-  for (int c = 0; c < kRegChunks; ++c) {
-    const int idx = threadIdx.x + c * kNT;
-    buf[c] = (idx < nvec) ? src[idx] : make_uint4(0xff80ff80u, 0xff80ff80u, 0xff80ff80u, 0xff80ff80u);
-  }
-  if (greedy) {
-#pragma unroll
-    for (int c = 0; c < kRegChunks; ++c) {
-      const int idx = threadIdx.x + c * kNT;
-      if (idx < nvec) {
-        const uint4 w = buf[c];
-        dst[2 * idx] = make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y));
-        dst[2 * idx + 1] = make_float4(bf16_lo(w.z), bf16_hi(w.z), bf16_lo(w.w), bf16_hi(w.w));
-      }
+      for (int e = 0; e < P; e += 4)
+        *reinterpret_cast<float4*>(dst + (int64_t)i * P + e) = make_float4(x[e], x[e + 1], x[e + 2], x[e + 3]);
     }
     return;
   }
-  // max(x / T) == max(x) / T for T > 0 (correctly rounded division is monotone);
-  // padding holds -inf.
-  float mx = -INFINITY;
+  const float a = 1.4426950408889634f / T;
+  float m = -INFINITY, s = 0.f;
+  int i = tid;
+  for (; i + (kUnroll - 1) * kVecNT < nvec; i += kUnroll * kVecNT) {
+    uint4 w[kUnroll];
 #pragma unroll
-  for (int c = 0; c < kRegChunks; ++c) {
-    const uint4 w = buf[c];
-    mx = fmaxf(mx, fmaxf(fmaxf(bf16_lo(w.x), bf16_hi(w.x)), fmaxf(bf16_lo(w.y), bf16_hi(w.y))));
-    mx = fmaxf(mx, fmaxf(fmaxf(bf16_lo(w.z), bf16_hi(w.z)), fmaxf(bf16_lo(w.w), bf16_hi(w.w))));
+    for (int u = 0; u < kUnroll; ++u) w[u] = src[i + u * kVecNT];
+    float lm = -INFINITY;
+    float x[kUnroll][P];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      Tr::expand(w[u], x[u]);
+#pragma unroll
+      for (int e = 0; e < P; ++e) lm = fmaxf(lm, x[u][e]);
+    }
+    const float mn = fmaxf(m, lm * a);
+    if (mn == -INFINITY) continue;  // every value so far is -inf
+    float acc = 0.f;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+      for (int e = 0; e < P; ++e) acc += __builtin_amdgcn_exp2f(__builtin_fmaf(x[u][e], a, -mn));
+    s = (m == -INFINITY ? 0.f : s * __builtin_amdgcn_exp2f(m - mn)) + acc;
+    m = mn;
   }
-  const float m = nvx::block_max<kNT>(mx, red) / T;
-  float s = 0.f;
+  for (; i < nvec; i += kVecNT) {
+    float x[P];
+    Tr::expand(src[i], x);
+    float lm = -INFINITY;
 #pragma unroll
-  for (int c = 0; c < kRegChunks; ++c) {
-    const int idx = threadIdx.x + c * kNT;
-    if (idx < nvec) {
-      const uint4 w = buf[c];
-      s += __expf(bf16_lo(w.x) / T - m) + __expf(bf16_hi(w.x) / T - m);
-      s += __expf(bf16_lo(w.y) / T - m) + __expf(bf16_hi(w.y) / T - m);
-      s += __expf(bf16_lo(w.z) / T - m) + __expf(bf16_hi(w.z) / T - m);
-      s += __expf(bf16_lo(w.w) / T - m) + __expf(bf16_hi(w.w) / T - m);
+    for (int e = 0; e < P; ++e) lm = fmaxf(lm, x[e]);
+    const float mn = fmaxf(m, lm * a);
+    if (mn == -INFINITY) continue;
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < P; ++e) acc += __builtin_amdgcn_exp2f(__builtin_fmaf(x[e], a, -mn));
+    s = (m == -INFINITY ? 0.f : s * __builtin_amdgcn_exp2f(m - mn)) + acc;
+    m = mn;
+  }
+  const float M = nvx::block_max<kVecNT>(m, red);
+  const float part = (m == -INFINITY) ? 0.f : s * __builtin_amdgcn_exp2f(m - M);
+  const float inv = 1.f / nvx::block_sum_any<kVecNT>(part, red);
+  i = tid;
+  for (; i + (kUnroll - 1) * kVecNT < nvec; i += kUnroll * kVecNT) {
+    uint4 w[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) w[u] = src[i + u * kVecNT];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      float x[P];
+      Tr::expand(w[u], x);
+      float* d = dst + (int64_t)(i + u * kVecNT) * P;
+#pragma unroll
+      for (int e = 0; e < P; e += 4)
+        *reinterpret_cast<float4*>(d + e) = make_float4(
+            __builtin_amdgcn_exp2f(__builtin_fmaf(x[e], a, -M)) * inv,
+            __builtin_amdgcn_exp2f(__builtin_fmaf(x[e + 1], a, -M)) * inv,
+            __builtin_amdgcn_exp2f(__builtin_fmaf(x[e + 2], a, -M)) * inv,
+            __builtin_amdgcn_exp2f(__builtin_fmaf(x[e + 3], a, -M)) * inv);
     }
   }
-  const float inv = 1.f / nvx::block_sum_any<kNT>(s, red);
+  for (; i < nvec; i += kVecNT) {
+    float x[P];
+    Tr::expand(src[i], x);
+    float* d = dst + (int64_t)i * P;
 #pragma unroll
-  for (int c = 0; c < kRegChunks; ++c) {
-    const int idx = threadIdx.x + c * kNT;
-    if (idx < nvec) {
-      const uint4 w = buf[c];
-      dst[2 * idx] = make_float4(__expf(bf16_lo(w.x) / T - m) * inv, __expf(bf16_hi(w.x) / T - m) * inv,
-                                 __expf(bf16_lo(w.y) / T - m) * inv, __expf(bf16_hi(w.y) / T - m) * inv);
-      dst[2 * idx + 1] =
-          make_float4(__expf(bf16_lo(w.z) / T - m) * inv, __expf(bf16_hi(w.z) / T - m) * inv,
-                      __expf(bf16_lo(w.w) / T - m) * inv, __expf(bf16_hi(w.w) / T - m) * inv);
-    }
+    for (int e = 0; e < P; e += 4)
+      *reinterpret_cast<float4*>(d + e) = make_float4(
+          __builtin_amdgcn_exp2f(__builtin_fmaf(x[e], a, -M)) * inv,
+          __builtin_amdgcn_exp2f(__builtin_fmaf(x[e + 1], a, -M)) * inv,
+          __builtin_amdgcn_exp2f(__builtin_fmaf(x[e + 2], a, -M)) * inv,
+          __builtin_amdgcn_exp2f(__builtin_fmaf(x[e + 3], a, -M)) * inv);
   }
 }
 
@@ -119,46 +177,46 @@ __global__ __launch_bounds__(kNT) void softmax_stream_kernel(const void* __restr
     for (int i = threadIdx.x; i < V; i += kNT) dst[i] = load_logit(src, i, dtype);
     return;
   }
+  // Online max / sum over the raw logits in log2 units (x * log2(e) / T).
+  const float a = 1.4426950408889634f / T;
   float m = -INFINITY, s = 0.f;
   for (int i = threadIdx.x; i < V; i += kNT) {
-    const float x = load_logit(src, i, dtype) / T;
+    const float x = load_logit(src, i, dtype) * a;
     if (x == -INFINITY) continue;
     if (x > m) {
-      s = s * __expf(m - x) + 1.f;
+      s = s * __builtin_amdgcn_exp2f(m - x) + 1.f;
       m = x;
     } else {
-      s += __expf(x - m);
+      s += __builtin_amdgcn_exp2f(x - m);
     }
   }
   const float M = nvx::block_max<kNT>(m, red);
-  const float part = (m == -INFINITY) ? 0.f : s * __expf(m - M);
+  const float part = (m == -INFINITY) ? 0.f : s * __builtin_amdgcn_exp2f(m - M);
   const float inv = 1.f / nvx::block_sum_any<kNT>(part, red);
-  for (int i = threadIdx.x; i < V; i += kNT) dst[i] = __expf(load_logit(src, i, dtype) / T - M) * inv;
+  for (int i = threadIdx.x; i < V; i += kNT)
+    dst[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(load_logit(src, i, dtype), a, -M)) * inv;
 }
 
 // ------------------------------------------------------- rejection sampling
-struct Chain {
-  const float* S;  // normalisers of the residual steps (LDS)
-  const int* X;    // rejected token of each step (LDS, delta mode)
-  int k;
+// Current distribution at a node (closed form, see the contract in the oracle):
+//   stochastic: cur[y] = max(p[y] - c*q[y], 0) / Z
+//   delta:      cur[y] = (y in R ? 0 : p[y]) / Z
+struct Residual {
+  float c, Z;
+  const int* R;  // rejected tokens (LDS), delta mode
+  int nR;
   bool delta;
 };
 
-// cur_k[y] from p[y], q[y] following the residual steps.
-__device__ __forceinline__ float chain_eval(const Chain& ch, float py, float qy, int y) {
-  float v = py;
-  for (int j = 0; j < ch.k; ++j) {
-    const float S = ch.S[j];
-    if (!(S > 0.f)) {
-      v = py;
-      continue;
-    }
-    if (ch.delta)
-      v = ((y == ch.X[j]) ? 0.f : v) / S;
-    else
-      v = fmaxf(v - qy, 0.f) / S;
-  }
-  return v;
+__device__ __forceinline__ bool in_set(const int* R, int n, int y) {
+  bool hit = false;
+  for (int i = 0; i < n; ++i) hit |= (R[i] == y);
+  return hit;
+}
+
+__device__ __forceinline__ float cur_eval(const Residual& r, float py, float qy, int y) {
+  if (r.delta) return (r.nR > 0 && in_set(r.R, r.nR, y) ? 0.f : py) / r.Z;
+  return fmaxf(py - r.c * qy, 0.f) / r.Z;
 }
 
 __device__ __forceinline__ void load4(const float* row, int g, int V, bool vec, float out[4]) {
@@ -172,44 +230,60 @@ __device__ __forceinline__ void load4(const float* row, int g, int V, bool vec, 
   }
 }
 
-// Canonical sum over y of the residual of the current distribution after also
-// rejecting token x: stochastic max(cur - q, 0); delta cur with x zeroed.
-__device__ float residual_sum(const float* prow, const float* qrow, int V, bool vec, const Chain& ch,
-                              int x, float* red) {
+// Canonical sum over y of max(p[y] - c*q[y], 0) (the un-normalised stochastic
+// residual for multiplier c).  Four groups per lane are loaded before they are
+// accumulated (in the same order) to keep more bytes in flight.
+__device__ float residual_sum(const float* prow, const float* qrow, int V, bool vec, float c,
+                              float* red) {
   const int G = (V + 3) / 4;
   float acc = 0.f;
-  for (int g = threadIdx.x; g < G; g += kNT) {
-    float p[4], q[4] = {0.f, 0.f, 0.f, 0.f};
-    load4(prow, g, V, vec, p);
-    if (!ch.delta) load4(qrow, g, V, vec, q);
+  int g = threadIdx.x;
+  for (; g + 3 * kNT < G; g += 4 * kNT) {
+    float p[4][4], q[4][4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int y = 4 * g + c;
-      if (y < V) {
-        const float v = chain_eval(ch, p[c], q[c], y);
-        const float r = ch.delta ? ((y == x) ? 0.f : v) : fmaxf(v - q[c], 0.f);
-        acc = acc + r;
-      }
+    for (int u = 0; u < 4; ++u) {
+      load4(prow, g + u * kNT, V, vec, p[u]);
+      load4(qrow, g + u * kNT, V, vec, q[u]);
     }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = acc + fmaxf(p[u][e] - c * q[u][e], 0.f);
+  }
+  for (; g < G; g += kNT) {
+    float p[4], q[4];
+    load4(prow, g, V, vec, p);
+    load4(qrow, g, V, vec, q);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (4 * g + e < V) acc = acc + fmaxf(p[e] - c * q[e], 0.f);
   }
   return nvx::block_sum_canonical<kNT>(acc, red);
 }
 
 // Inverse-CDF pick from the current distribution with uniform u (contract in
 // oracle/sampler.py: cdf_pick).
-__device__ int cdf_pick(const float* prow, const float* qrow, int V, bool vec, const Chain& ch, float u,
-                        float* red, int* redi, float* incl_lds) {
+__device__ int cdf_pick(const float* prow, const float* qrow, int V, bool vec, const Residual& r,
+                        float u, float* red, int* redi, float* incl_lds) {
   const int C = 4 * (((V + 3) / 4 + kNT - 1) / kNT);
   const int lo = threadIdx.x * C;
   const int hi = min(lo + C, V);
+  // Lane t owns elements [lo, hi); its groups are read four at a time.
   float s = 0.f;
-  for (int i = lo; i < hi; i += 4) {
-    float p[4], q[4] = {0.f, 0.f, 0.f, 0.f};
-    load4(prow, i / 4, V, vec, p);
-    if (!ch.delta) load4(qrow, i / 4, V, vec, q);
+  for (int i = lo; i < hi; i += 16) {
+    float p[4][4], q[4][4] = {};
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-      if (i + c < hi) s = s + chain_eval(ch, p[c], q[c], i + c);
+    for (int u = 0; u < 4; ++u) {
+      if (i + 4 * u < hi) {
+        load4(prow, i / 4 + u, V, vec, p[u]);
+        if (!r.delta) load4(qrow, i / 4 + u, V, vec, q[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (i + 4 * u + e < hi) s = s + cur_eval(r, p[u][e], q[u][e], i + 4 * u + e);
   }
   float total;
   const float incl = nvx::block_incl_scan_canonical<kNT>(s, red, &total);
@@ -218,18 +292,27 @@ __device__ int cdf_pick(const float* prow, const float* qrow, int V, bool vec, c
   const float tau = u * total;
   float run = threadIdx.x > 0 ? incl_lds[threadIdx.x - 1] : 0.f;
   int first = INT32_MAX, last = -1;
-  for (int i = lo; i < hi; i += 4) {
-    float p[4], q[4] = {0.f, 0.f, 0.f, 0.f};
-    load4(prow, i / 4, V, vec, p);
-    if (!ch.delta) load4(qrow, i / 4, V, vec, q);
+  for (int i = lo; i < hi; i += 16) {
+    float p[4][4], q[4][4] = {};
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if (i + c < hi) {
-        const float v = chain_eval(ch, p[c], q[c], i + c);
-        run = run + v;
-        if (v > 0.f) {
-          last = i + c;
-          if (first == INT32_MAX && run > tau) first = i + c;
+    for (int u = 0; u < 4; ++u) {
+      if (i + 4 * u < hi) {
+        load4(prow, i / 4 + u, V, vec, p[u]);
+        if (!r.delta) load4(qrow, i / 4 + u, V, vec, q[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int y = i + 4 * u + e;
+        if (y < hi) {
+          const float v = cur_eval(r, p[u][e], q[u][e], y);
+          run = run + v;
+          if (v > 0.f) {
+            last = y;
+            if (first == INT32_MAX && run > tau) first = y;
+          }
         }
       }
     }
@@ -245,15 +328,22 @@ __device__ int block_argmax(const float* row, int V, bool vec, float* red, int* 
   float bv = -INFINITY;
   int bi = INT32_MAX;
   const int G = (V + 3) / 4;
-  for (int g = threadIdx.x; g < G; g += kNT) {
-    float p[4];
-    load4(row, g, V, vec, p);
+  for (int g0 = threadIdx.x; g0 < G; g0 += 4 * kNT) {
+    float p[4][4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int y = 4 * g + c;
-      if (y < V && (p[c] > bv || (p[c] == bv && y < bi))) {
-        bv = p[c];
-        bi = y;
+    for (int u = 0; u < 4; ++u)
+      if (g0 + u * kNT < G) load4(row, g0 + u * kNT, V, vec, p[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int g = g0 + u * kNT;
+      if (g >= G) break;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int y = 4 * g + c;
+        if (y < V && (p[u][c] > bv || (p[u][c] == bv && y < bi))) {
+          bv = p[u][c];
+          bi = y;
+        }
       }
     }
   }
@@ -300,8 +390,7 @@ __global__ __launch_bounds__(kNT) void rejection_tree_kernel(
   __shared__ int redi[kNW];
   __shared__ int s_par[kMaxNodes], s_tok[kMaxNodes], s_path[kMaxNodes];
   __shared__ float s_u[kMaxNodes];
-  __shared__ float s_S[kMaxNodes];
-  __shared__ int s_X[kMaxNodes];
+  __shared__ int s_R[kMaxNodes];
   __shared__ float s_incl[kNT];
 
   const int b = blockIdx.x;
@@ -334,30 +423,48 @@ __global__ __launch_bounds__(kNT) void rejection_tree_kernel(
         break;
       }
     } else {
-      Chain ch{s_S, s_X, 0, delta != 0};
+      Residual res{0.f, 1.f, s_R, 0, delta != 0};
       for (int j = cur + 1; j < T; ++j) {
         if (s_par[j] != cur) continue;
         const int x = s_tok[j];
-        float cx = 0.f, qx = 1.f;
-        if (x >= 0 && x < V) {
-          const float qv = ch.delta ? 0.f : qrow[x];
-          cx = chain_eval(ch, prow[x], qv, x);
-          if (!ch.delta) qx = qv;
+        const bool valid = x >= 0 && x < V;
+        float cx = 0.f, qx = 1.f, px = 0.f;
+        if (valid) {
+          px = prow[x];
+          const float qv = res.delta ? 0.f : qrow[x];
+          cx = cur_eval(res, px, qv, x);
+          if (!res.delta) qx = qv;
         }
         if (s_u[j] * qx <= cx && cx > 0.f) {
           accepted = j;
           break;
         }
-        const float S = residual_sum(prow, qrow, V, vec, ch, x, red);
-        if (threadIdx.x == 0) {
-          s_S[ch.k] = S;
-          s_X[ch.k] = x;
+        if (res.delta) {
+          if (valid && !(res.nR > 0 && in_set(s_R, res.nR, x))) {
+            __syncthreads();  // every lane has read s_R
+            if (threadIdx.x == 0) s_R[res.nR] = x;
+            __syncthreads();
+            res.nR += 1;
+            res.Z = res.Z - px;
+          }
+          if (!(res.Z > 0.f)) {
+            res.nR = 0;
+            res.Z = 1.f;
+          }
+        } else {
+          const float c = res.c + res.Z;
+          const float Z = residual_sum(prow, qrow, V, vec, c, red);
+          if (Z > 0.f) {
+            res.c = c;
+            res.Z = Z;
+          } else {
+            res.c = 0.f;
+            res.Z = 1.f;
+          }
         }
-        __syncthreads();
-        ch.k += 1;
       }
       if (accepted < 0) {
-        next = cdf_pick(prow, qrow, V, vec, ch, uf, red, redi, s_incl);
+        next = cdf_pick(prow, qrow, V, vec, res, uf, red, redi, s_incl);
         break;
       }
     }
@@ -397,12 +504,15 @@ extern "C" int nvx_temperature_softmax(const void* logits, int32_t logits_dtype,
   NVX_CHECK(logits && temperatures && probs, "temperature_softmax: null pointer");
   hipStream_t s = (hipStream_t)stream;
   nvx::TimerScope timer(NVX_TIMER_SOFTMAX, s);
-  const bool regs = logits_dtype == NVX_DTYPE_BF16 && vocab % 8 == 0 &&
-                    logits_row_stride % 8 == 0 && vocab <= kNT * 8 * kRegChunks &&
-                    aligned16(logits) && aligned16(probs);
-  if (regs) {
-    hipLaunchKernelGGL(softmax_bf16_regs_kernel, dim3(num_rows), dim3(kNT), 0, s,
+  const int per = logits_dtype == NVX_DTYPE_BF16 ? 8 : 4;
+  const bool vec = vocab % per == 0 && logits_row_stride % per == 0 && aligned16(logits) &&
+                   aligned16(probs);
+  if (vec && logits_dtype == NVX_DTYPE_BF16) {
+    hipLaunchKernelGGL(softmax_vec_kernel<uint16_t>, dim3(num_rows), dim3(kVecNT), 0, s,
                        (const uint16_t*)logits, logits_row_stride, temperatures, probs, vocab);
+  } else if (vec) {
+    hipLaunchKernelGGL(softmax_vec_kernel<float>, dim3(num_rows), dim3(kVecNT), 0, s,
+                       (const float*)logits, logits_row_stride, temperatures, probs, vocab);
   } else {
     hipLaunchKernelGGL(softmax_stream_kernel, dim3(num_rows), dim3(kNT), 0, s, logits, logits_dtype,
                        logits_row_stride, temperatures, probs, vocab);

@@ -13,14 +13,21 @@ the contract below is restated from the published algorithms:
   rejection replaces it by norm(max(cur - q, 0)); an accepted child becomes the
   current node with distribution P[child].
 
-Exact fp32 contract (shared with the HIP kernel so integer outputs are bit-exact):
+Exact fp32 contract (shared with the HIP kernel so integer outputs are bit-exact).
+At the current node the distribution is tracked in closed form:
 
+* stochastic mode: ``cur[y] = max(p[y] - c*q[y], 0) / Z`` with scalars (c, Z),
+  starting at (0, 1).  Rejecting a child replaces cur by norm(max(cur - q, 0)),
+  which in exact arithmetic is the same form with ``c <- c + Z`` and
+  ``Z <- canonical_sum_y(max(p[y] - c*q[y], 0))`` (products and differences are
+  separately rounded fp32 operations).  If the new Z is not > 0 the distribution
+  falls back to P[cur] (c, Z = 0, 1).
+* delta mode (children are deterministic proposals, q is a point mass on the
+  child's token): ``cur[y] = (y in R ? 0 : p[y]) / Z``; rejecting a token x not
+  yet in R adds it to R and sets ``Z <- Z - p[x]`` (fp32, starting at 1); if Z
+  is not > 0 the distribution falls back to P[cur] (R empty, Z = 1).
 * acceptance of child c with token x: ``U[c] * q[x] <= cur[x] and cur[x] > 0``
-  (``q[x]`` is 1 in delta mode, where the children are deterministic proposals);
-* residual step j: ``cur_j[y] = max(cur_{j-1}[y] - q[y], 0) / S_j`` (delta mode:
-  ``cur_j[y] = (y == x_j ? 0 : cur_{j-1}[y]) / S_j``), with ``S_j`` the
-  ``canonical_sum`` of the un-normalised residual; if ``S_j`` is not > 0 the
-  distribution falls back to ``P[cur]``;
+  (``q[x]`` is 1 in delta mode); a token outside [0, V) is rejected;
 * the final token is ``cdf_pick(cur, U_final)``;
 * greedy rows (temperature 0): child accepted iff its token equals the first
   index of the maximum of the row; otherwise the next token is that index.
@@ -146,36 +153,39 @@ def first_argmax(row):
 
 
 # ------------------------------------------------------------------- tree sampling
-class _Chain:
-    """Residual chain cur_0 = p, cur_j = step_j(cur_{j-1})."""
+class _Residual:
+    """Current distribution at a node, in the closed form of the contract above."""
 
     def __init__(self, p, q, delta):
         self.p, self.q, self.delta = p, q, delta
-        self.steps = []  # (S_j, x_j); S_j <= 0 means fall back to p
+        self.c, self.Z = F32(0), F32(1)
+        self.R = []
 
     def eval(self, ys=None):
-        v = self.p if ys is None else self.p[ys]
-        for S, x in self.steps:
-            if not S > 0:
-                v = self.p if ys is None else self.p[ys]
-                continue
-            if self.delta:
-                yy = np.arange(self.p.shape[0]) if ys is None else ys
-                v = np.where(yy == x, F32(0), v) / S
-            else:
-                qq = self.q if ys is None else self.q[ys]
-                v = np.maximum(v - qq, F32(0)) / S
-        return v.astype(F32)
+        p = self.p if ys is None else self.p[ys]
+        if self.delta:
+            yy = np.arange(self.p.shape[0]) if ys is None else np.asarray(ys)
+            out = np.where(np.isin(yy, self.R), F32(0), p) / self.Z
+        else:
+            q = self.q if ys is None else self.q[ys]
+            out = np.maximum(p - self.c * q, F32(0)) / self.Z
+        return out.astype(F32)
 
     def reject(self, x):
-        cur = self.eval()
+        V = self.p.shape[0]
         if self.delta:
-            r = cur.copy()
-            if 0 <= x < r.shape[0]:
-                r[x] = 0
+            if 0 <= x < V and x not in self.R:
+                self.R.append(x)
+                self.Z = F32(self.Z - self.p[x])
+            if not self.Z > 0:
+                self.R, self.Z = [], F32(1)
         else:
-            r = np.maximum(cur - self.q, F32(0))
-        self.steps.append((canonical_sum(r), x))
+            c = F32(self.c + self.Z)
+            Z = canonical_sum(np.maximum(self.p - c * self.q, F32(0)))
+            if Z > 0:
+                self.c, self.Z = c, Z
+            else:
+                self.c, self.Z = F32(0), F32(1)
 
 
 def sample_tree_one(P, Q, tokens, parents, U, u_final, greedy, delta=False):
@@ -199,7 +209,7 @@ def sample_tree_one(P, Q, tokens, parents, U, u_final, greedy, delta=False):
             continue
         p = np.asarray(P[cur], dtype=F32)
         q = None if delta else np.asarray(Q[cur], dtype=F32)
-        chain = _Chain(p, q, delta)
+        chain = _Residual(p, q, delta)
         accepted = None
         V = p.shape[0]
         for c in kids:
