@@ -1,0 +1,207 @@
+"""ModelRunner: one process driving one GPU.
+
+Follows the reference's runner (nanovllm/engine/model_runner.py:15-220): paged KV
+allocation, host-side packing of the batch, the model forward and sampling.  Tensor
+parallel workers, the shm RPC and CUDA-graph capture are left out.
+
+Speculative decoding (``speculative_method="ngram"``) replaces the decode step by
+a verify step:
+
+1. the n-gram drafter proposes up to k tokens per sequence from its history
+   (``nvx_ngram_propose`` over the packed histories);
+2. each sequence's root (its last token, not yet cached) and draft tokens form a
+   chain of T = 1 + max draft length rows at positions ctx .. ctx+T-1; their K/V
+   are stored first and attended with the chain mask (``nvx_tree_attention``);
+3. the target rows are softmaxed at each sequence's temperature and verified
+   (``nvx_rejection_sample_tree``; delta mode: n-gram drafts are deterministic
+   proposals); greedy sequences accept while the draft matches the argmax;
+4. the accepted tokens plus one recovered/bonus token go back to the scheduler.
+A chain's accepted path is already contiguous, so no compaction is needed.
+"""
+import glob
+import os
+
+import numpy as np
+import torch
+
+from nanovllm.config import Config
+from nanovllm.engine.sequence import Sequence
+from nanovllm.layers.sampler import RejectionSampler, Sampler
+from nanovllm.models.qwen3 import Qwen3ForCausalLM, random_init_
+from nanovllm.spec.ngram import NgramProposer
+from nanovllm.spec.tree import ancestor_masks, chain_parents
+from nanovllm.utils.context import get_context, reset_context, set_context
+
+
+def _pinned(values, dtype):
+    return torch.tensor(values, dtype=dtype, pin_memory=True).cuda(non_blocking=True)
+
+
+class ModelRunner:
+
+    def __init__(self, config: Config, rank: int = 0, event=None):
+        self.config = config
+        hf_config = config.hf_config
+        self.block_size = config.kvcache_block_size
+        self.enforce_eager = True
+        self.world_size = 1
+        self.rank = rank
+        torch.cuda.set_device(rank)
+        default_dtype = torch.get_default_dtype()
+        torch.set_default_dtype(getattr(hf_config, "dtype", None) or torch.bfloat16)
+        torch.set_default_device("cuda")
+        self.model = Qwen3ForCausalLM(hf_config)
+        self.load_or_init(config.model)
+        self.sampler = Sampler()
+        self.rejection = RejectionSampler()
+        self.allocate_kv_cache()
+        torch.set_default_device("cpu")
+        torch.set_default_dtype(default_dtype)
+        self.proposer = None
+        if config.speculative_method == "ngram":
+            self.proposer = NgramProposer(config.ngram_max, config.ngram_min,
+                                          config.num_speculative_tokens)
+        self.gen = torch.Generator(device="cuda").manual_seed(config.seed)
+
+    def load_or_init(self, path):
+        files = glob.glob(os.path.join(path, "*.safetensors")) if path and os.path.isdir(path) else []
+        if not files:
+            random_init_(self.model, seed=self.config.seed)
+            return
+        from safetensors import safe_open
+        params = dict(self.model.named_parameters())
+        packed = {"q_proj": ("qkv_proj", 0), "k_proj": ("qkv_proj", 1), "v_proj": ("qkv_proj", 2),
+                  "gate_proj": ("gate_up_proj", 0), "up_proj": ("gate_up_proj", 1)}
+        cfg = self.config.hf_config
+        hd = getattr(cfg, "head_dim", cfg.hidden_size // cfg.num_attention_heads)
+        sizes = {"qkv_proj": [cfg.num_attention_heads * hd, cfg.num_key_value_heads * hd,
+                              cfg.num_key_value_heads * hd],
+                 "gate_up_proj": [cfg.intermediate_size, cfg.intermediate_size]}
+        for f in files:
+            with safe_open(f, "pt", "cpu") as fh:
+                for name in fh.keys():
+                    w = fh.get_tensor(name)
+                    for k, (fused, idx) in packed.items():
+                        if k in name:
+                            tgt = params[name.replace(k, fused)]
+                            off = sum(sizes[fused][:idx])
+                            tgt.data[off:off + sizes[fused][idx]].copy_(w)
+                            break
+                    else:
+                        if name in params:
+                            params[name].data.copy_(w)
+
+    def exit(self):
+        torch.cuda.synchronize()
+
+    def call(self, method_name, *args):
+        return getattr(self, method_name)(*args)
+
+    def allocate_kv_cache(self):
+        config = self.config
+        hf = config.hf_config
+        Hkv = hf.num_key_value_heads
+        D = getattr(hf, "head_dim", hf.hidden_size // hf.num_attention_heads)
+        dtype = torch.get_default_dtype()
+        block_bytes = 2 * hf.num_hidden_layers * self.block_size * Hkv * D * dtype.itemsize
+        if config.num_kvcache_blocks <= 0:
+            free, total = torch.cuda.mem_get_info()
+            reserve = 8 << 30  # activations, logits and fp32 probabilities of a step
+            config.num_kvcache_blocks = int(free * config.gpu_memory_utilization - reserve) // block_bytes
+        assert config.num_kvcache_blocks > 0
+        self.kv_cache = torch.empty(2, hf.num_hidden_layers, config.num_kvcache_blocks,
+                                    self.block_size, Hkv, D)
+        for l, attn in enumerate(self.model.attention_layers()):
+            attn.k_cache = self.kv_cache[0, l]
+            attn.v_cache = self.kv_cache[1, l]
+
+    def prepare_block_tables(self, seqs: list[Sequence]):
+        max_len = max(len(seq.block_table) for seq in seqs)
+        block_tables = [seq.block_table + [-1] * (max_len - len(seq.block_table)) for seq in seqs]
+        return _pinned(block_tables, torch.int32)
+
+    def prepare_prefill(self, seqs: list[Sequence]):
+        input_ids, positions, slot_mapping, ctx_lens = [], [], [], []
+        cu_seqlens_q, cu_seqlens_k = [0], [0]
+        max_seqlen_q = max_seqlen_k = 0
+        for seq in seqs:
+            start = seq.num_cached_tokens
+            end = start + seq.num_scheduled_tokens
+            input_ids.extend(seq[start:end])
+            positions.extend(range(start, end))
+            cu_seqlens_q.append(cu_seqlens_q[-1] + end - start)
+            cu_seqlens_k.append(cu_seqlens_k[-1] + end)
+            max_seqlen_q = max(end - start, max_seqlen_q)
+            max_seqlen_k = max(end, max_seqlen_k)
+            ctx_lens.append(end)
+            bt = np.asarray(seq.block_table, np.int64)
+            pos = np.arange(start, end)
+            slot_mapping.extend((bt[pos // self.block_size] * self.block_size
+                                 + pos % self.block_size).tolist())
+        set_context(True, _pinned(cu_seqlens_q, torch.int32), _pinned(cu_seqlens_k, torch.int32),
+                    max_seqlen_q, max_seqlen_k, _pinned(slot_mapping, torch.int32),
+                    _pinned(ctx_lens, torch.int32), self.prepare_block_tables(seqs))
+        return _pinned(input_ids, torch.int64), _pinned(positions, torch.int64)
+
+    def prepare_decode(self, seqs: list[Sequence], drafts=None):
+        """Rows per sequence: the root (last token) then its draft tokens (a chain)."""
+        T = 1 + (max(len(d) for d in drafts) if drafts else 0)
+        input_ids, positions, slot_mapping, context_lens, num_nodes = [], [], [], [], []
+        for i, seq in enumerate(seqs):
+            ctx = len(seq) - 1
+            d = drafts[i] if drafts else []
+            toks = [seq.last_token] + d + [0] * (T - 1 - len(d))
+            input_ids.extend(toks)
+            positions.extend(range(ctx, ctx + T))
+            bt = seq.block_table
+            for p in range(ctx, ctx + T):
+                slot_mapping.append(bt[p // self.block_size] * self.block_size + p % self.block_size)
+            context_lens.append(ctx + T)
+            num_nodes.append(1 + len(d))
+        B = len(seqs)
+        masks = np.tile(ancestor_masks(chain_parents(T)), B) if T > 1 else None
+        set_context(False, cu_seqlens_q=_pinned(list(range(0, B * T + 1, T)), torch.int32),
+                    max_seqlen_q=T, slot_mapping=_pinned(slot_mapping, torch.int32),
+                    context_lens=_pinned(context_lens, torch.int32),
+                    block_tables=self.prepare_block_tables(seqs),
+                    tree_mask=None if masks is None else _pinned(masks.tolist(), torch.int64),
+                    max_context_len=max(context_lens))
+        return (_pinned(input_ids, torch.int64), _pinned(positions, torch.int64), T,
+                _pinned(num_nodes, torch.int32))
+
+    def prepare_sample(self, seqs: list[Sequence]):
+        return _pinned([seq.temperature for seq in seqs], torch.float32)
+
+    @torch.inference_mode()
+    def run_model(self, input_ids, positions, is_prefill):
+        hidden = self.model(input_ids, positions)
+        if is_prefill:  # logits of each sequence's last scheduled token only
+            cu = get_context().cu_seqlens_q
+            hidden = hidden[cu[1:].long() - 1]
+        return self.model.compute_logits(hidden)
+
+    @torch.inference_mode()
+    def run(self, seqs: list[Sequence], is_prefill: bool):
+        if is_prefill:
+            input_ids, positions = self.prepare_prefill(seqs)
+            temperatures = self.prepare_sample(seqs)
+            logits = self.run_model(input_ids, positions, True)
+            token_ids = self.sampler(logits, temperatures).tolist()
+            reset_context()
+            return token_ids
+        drafts = self.proposer.propose([seq.token_ids for seq in seqs]) if self.proposer else None
+        input_ids, positions, T, num_nodes = self.prepare_decode(seqs, drafts)
+        temperatures = self.prepare_sample(seqs)
+        logits = self.run_model(input_ids, positions, False)
+        reset_context()
+        B = len(seqs)
+        if T == 1:
+            return [[t] for t in self.sampler(logits, temperatures).tolist()]
+        tokens = input_ids.view(B, T).to(torch.int32)
+        parents = torch.from_numpy(np.tile(chain_parents(T), (B, 1))).cuda()
+        U = torch.rand(B, T, device="cuda", generator=self.gen)
+        Uf = torch.rand(B, device="cuda", generator=self.gen)
+        _, acc, out_tokens, _ = self.rejection(logits, temperatures, None, tokens, parents, U, Uf,
+                                               num_nodes)
+        acc, out_tokens = acc.tolist(), out_tokens.tolist()
+        return [out_tokens[b][:acc[b] + 1] for b in range(B)]
