@@ -155,6 +155,33 @@ int nvx_rejection_sample_tree(const float* target_probs, int64_t p_seq_stride,
                               int32_t* path, int32_t* accepted_len, int32_t* out_tokens,
                               int32_t* next_token, void* stream);
 
+/* -------------------------------------------------- fused model layers --
+ * Elementwise layers of the target model around the verify-path attention, each
+ * one pass over HBM (bf16 in/out, fp32 math).  Not part of the four verify-path
+ * kernels; they replace chains of eager torch kernels.
+ *
+ * nvx_rmsnorm: RMSNorm / add+RMSNorm (reference nanovllm/layers/layernorm.py:16-40):
+ *   s = x (+ residual); residual_out = bf16(s); out = bf16(bf16(s*rsqrt(mean(s^2)+eps))*w).
+ *   residual and residual_out are both NULL (plain) or both set.  hidden % 8 == 0,
+ *   hidden <= 8192, 16-byte aligned rows.
+ * nvx_qk_norm_rope: per-head RMSNorm of the q and k heads of a fused qkv row, then
+ *   NeoX rotary embedding at positions[n] with cos_sin_cache [max_pos, 128] fp32
+ *   (64 cos then 64 sin) (reference qwen3.py:82-85, rotary_embedding.py:6-14);
+ *   writes contiguous q_out [N, Hq, 128] and k_out [N, Hkv, 128].  head_dim 128.
+ * nvx_silu_mul: out[n, i] = bf16(silu(gate_up[n, i]) * gate_up[n, inter + i])
+ *   (reference nanovllm/layers/activation.py:8-11).
+ */
+int nvx_rmsnorm(const void* x, int64_t x_row_stride, const void* residual, void* residual_out,
+                const void* weight, void* out, int32_t num_rows, int32_t hidden, float eps,
+                void* stream);
+int nvx_qk_norm_rope(const void* qkv, int64_t qkv_row_stride, int32_t num_q_heads,
+                     int32_t num_kv_heads, int32_t head_dim, const void* q_norm_weight,
+                     const void* k_norm_weight, const int64_t* positions,
+                     const float* cos_sin_cache, int32_t num_tokens, void* q_out, void* k_out,
+                     float eps, void* stream);
+int nvx_silu_mul(const void* gate_up, int64_t row_stride, void* out, int32_t num_rows,
+                 int32_t inter, void* stream);
+
 /* ------------------------------------------------------------------ timing --
  * Optional per-entry-point HIP-event timing on the launch stream (used by the
  * benchmark to measure kernel durations in its timed region).

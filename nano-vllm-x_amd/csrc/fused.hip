@@ -1,0 +1,199 @@
+// Fused elementwise layers of the target model (bf16 in/out, fp32 math).
+//
+// These replace chains of eager torch kernels around the verify path's attention:
+//   rmsnorm      : RMSNorm and add+RMSNorm   (reference nanovllm/layers/layernorm.py:16-40)
+//   qk_norm_rope : per-head q/k RMSNorm then NeoX RoPE (qwen3.py:82-85,
+//                  rotary_embedding.py:6-14, :37-48), writing contiguous q and k
+//   silu_mul     : SiLU(gate) * up           (activation.py:8-11)
+// Each is one pass over HBM: read the inputs once, write the outputs once.
+#include "nvx_internal.h"
+
+namespace {
+
+__device__ __forceinline__ float bf(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+__device__ __forceinline__ uint16_t f2bf(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // NaN stays NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float rbf(float x) { return bf(f2bf(x)); }  // round to bf16
+
+constexpr int kNormNT = 256;
+
+// One workgroup per row; each thread owns 8-element (16-byte) pieces.
+// plain: y = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w)
+// add:   s = x + r (fp32); r_out = bf16(s); y from s as above.
+__global__ __launch_bounds__(kNormNT) void rmsnorm_kernel(const uint16_t* __restrict__ x,
+                                                          int64_t x_stride,
+                                                          const uint16_t* __restrict__ res,
+                                                          uint16_t* __restrict__ res_out,
+                                                          const uint16_t* __restrict__ w,
+                                                          uint16_t* __restrict__ out, int H,
+                                                          float eps) {
+  __shared__ float red[kNormNT / nvx::kWave];
+  const int row = blockIdx.x;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + (int64_t)row * x_stride);
+  const uint4* rr = res ? reinterpret_cast<const uint4*>(res + (int64_t)row * H) : nullptr;
+  const int nv = H / 8;
+  constexpr int kMaxPer = 4;  // H <= 256*8*4 = 8192
+  float v[kMaxPer][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < kMaxPer; ++c) {
+    const int i = threadIdx.x + c * kNormNT;
+    if (i < nv) {
+      const uint4 a = xr[i];
+      const uint16_t* ah = reinterpret_cast<const uint16_t*>(&a);
+      uint4 b = make_uint4(0, 0, 0, 0);
+      if (rr) b = rr[i];
+      const uint16_t* bh = reinterpret_cast<const uint16_t*>(&b);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float s = bf(ah[e]);
+        if (rr) s = s + bf(bh[e]);
+        v[c][e] = s;
+        ss += s * s;
+      }
+      if (res_out) {
+        uint4 o;
+        uint16_t* oh = reinterpret_cast<uint16_t*>(&o);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) oh[e] = f2bf(v[c][e]);
+        reinterpret_cast<uint4*>(res_out + (int64_t)row * H)[i] = o;
+      }
+    }
+  }
+  const float inv = rsqrtf(nvx::block_sum_any<kNormNT>(ss, red) / (float)H + eps);
+  const uint4* wr = reinterpret_cast<const uint4*>(w);
+#pragma unroll
+  for (int c = 0; c < kMaxPer; ++c) {
+    const int i = threadIdx.x + c * kNormNT;
+    if (i < nv) {
+      const uint4 ww = wr[i];
+      const uint16_t* wh = reinterpret_cast<const uint16_t*>(&ww);
+      uint4 o;
+      uint16_t* oh = reinterpret_cast<uint16_t*>(&o);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) oh[e] = f2bf(rbf(v[c][e] * inv) * bf(wh[e]));
+      reinterpret_cast<uint4*>(out + (int64_t)row * H)[i] = o;
+    }
+  }
+}
+
+// One wave per (token, head) of q and k; lane l owns elements l and l + 64, which
+// are exactly the pair NeoX RoPE rotates together (head_dim 128).
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(
+    const uint16_t* __restrict__ qkv, int64_t row_stride, int Hq, int Hkv,
+    const uint16_t* __restrict__ qw, const uint16_t* __restrict__ kw,
+    const int64_t* __restrict__ positions, const float* __restrict__ cos_sin, int N,
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_out, float eps) {
+  const int H = Hq + Hkv;
+  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);  // global wave id
+  if (gw >= N * H) return;
+  const int lane = threadIdx.x & 63;
+  const int n = gw / H, h = gw % H;
+  const bool isq = h < Hq;
+  const uint16_t* src = qkv + (int64_t)n * row_stride + (int64_t)h * 128;
+  const float x1 = bf(src[lane]), x2 = bf(src[lane + 64]);
+  float ss = x1 * x1 + x2 * x2;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += nvx::shfl_xor_f(ss, off);
+  const float inv = rsqrtf(ss / 128.f + eps);
+  const uint16_t* w = isq ? qw : kw;
+  const float y1 = rbf(rbf(x1 * inv) * bf(w[lane]));
+  const float y2 = rbf(rbf(x2 * inv) * bf(w[lane + 64]));
+  const float* cs = cos_sin + positions[n] * 128;
+  const float c = cs[lane], s = cs[64 + lane];
+  const float o1 = y1 * c - y2 * s;
+  const float o2 = y2 * c + y1 * s;
+  uint16_t* dst = isq ? q_out + ((int64_t)n * Hq + h) * 128 : k_out + ((int64_t)n * Hkv + (h - Hq)) * 128;
+  dst[lane] = f2bf(o1);
+  dst[lane + 64] = f2bf(o2);
+}
+
+// out[n, i] = bf16(silu(gate) * up), gate = gu[n, i], up = gu[n, I + i]; 8 per thread.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gu,
+                                                       int64_t stride, uint16_t* __restrict__ out,
+                                                       int N, int I) {
+  const int nv = I / 8;
+  const int64_t total = (int64_t)N * nv;
+  for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += (int64_t)gridDim.x * 256) {
+    const int n = (int)(t / nv), i = (int)(t - (int64_t)n * nv);
+    const uint4 g = reinterpret_cast<const uint4*>(gu + (int64_t)n * stride)[i];
+    const uint4 u = reinterpret_cast<const uint4*>(gu + (int64_t)n * stride + I)[i];
+    const uint16_t* gh = reinterpret_cast<const uint16_t*>(&g);
+    const uint16_t* uh = reinterpret_cast<const uint16_t*>(&u);
+    uint4 o;
+    uint16_t* oh = reinterpret_cast<uint16_t*>(&o);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float a = bf(gh[e]);
+      oh[e] = f2bf(a / (1.f + __expf(-a)) * bf(uh[e]));
+    }
+    reinterpret_cast<uint4*>(out + (int64_t)n * I)[i] = o;
+  }
+}
+
+inline bool a16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+extern "C" int nvx_rmsnorm(const void* x, int64_t x_row_stride, const void* residual,
+                           void* residual_out, const void* weight, void* out, int32_t num_rows,
+                           int32_t hidden, float eps, void* stream) {
+  nvx::clear_error();
+  NVX_CHECK(hidden > 0 && hidden % 8 == 0 && hidden <= kNormNT * 8 * 4,
+            "rmsnorm: hidden must be a multiple of 8 and <= %d (got %d)", kNormNT * 32, hidden);
+  NVX_CHECK(num_rows >= 0 && x_row_stride % 8 == 0, "rmsnorm: bad rows/stride");
+  NVX_CHECK((residual == nullptr) == (residual_out == nullptr),
+            "rmsnorm: residual and residual_out go together");
+  if (num_rows == 0) return NVX_OK;
+  NVX_CHECK(x && weight && out && a16(x) && a16(weight) && a16(out) &&
+                (!residual || (a16(residual) && a16(residual_out))),
+            "rmsnorm: null or unaligned pointer");
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(num_rows), dim3(kNormNT), 0, s, (const uint16_t*)x,
+                     x_row_stride, (const uint16_t*)residual, (uint16_t*)residual_out,
+                     (const uint16_t*)weight, (uint16_t*)out, hidden, eps);
+  NVX_LAUNCHED();
+  return NVX_OK;
+}
+
+extern "C" int nvx_qk_norm_rope(const void* qkv, int64_t qkv_row_stride, int32_t num_q_heads,
+                                int32_t num_kv_heads, int32_t head_dim, const void* q_norm_weight,
+                                const void* k_norm_weight, const int64_t* positions,
+                                const float* cos_sin_cache, int32_t num_tokens, void* q_out,
+                                void* k_out, float eps, void* stream) {
+  nvx::clear_error();
+  NVX_CHECK(head_dim == 128, "qk_norm_rope: head_dim must be 128 (got %d)", head_dim);
+  NVX_CHECK(num_tokens >= 0 && num_q_heads > 0 && num_kv_heads > 0, "qk_norm_rope: bad sizes");
+  if (num_tokens == 0) return NVX_OK;
+  NVX_CHECK(qkv && q_norm_weight && k_norm_weight && positions && cos_sin_cache && q_out && k_out,
+            "qk_norm_rope: null pointer");
+  const int64_t waves = (int64_t)num_tokens * (num_q_heads + num_kv_heads);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s,
+                     (const uint16_t*)qkv, qkv_row_stride, num_q_heads, num_kv_heads,
+                     (const uint16_t*)q_norm_weight, (const uint16_t*)k_norm_weight, positions,
+                     cos_sin_cache, num_tokens, (uint16_t*)q_out, (uint16_t*)k_out, eps);
+  NVX_LAUNCHED();
+  return NVX_OK;
+}
+
+extern "C" int nvx_silu_mul(const void* gate_up, int64_t row_stride, void* out, int32_t num_rows,
+                            int32_t inter, void* stream) {
+  nvx::clear_error();
+  NVX_CHECK(inter > 0 && inter % 8 == 0 && row_stride % 8 == 0 && num_rows >= 0,
+            "silu_mul: inter and stride must be multiples of 8");
+  if (num_rows == 0) return NVX_OK;
+  NVX_CHECK(gate_up && out && a16(gate_up) && a16(out), "silu_mul: null or unaligned pointer");
+  const int64_t work = (int64_t)num_rows * (inter / 8);
+  int64_t grid = (work + 255) / 256;
+  if (grid > 65536) grid = 65536;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)grid), dim3(256), 0, s,
+                     (const uint16_t*)gate_up, row_stride, (uint16_t*)out, num_rows, inter);
+  NVX_LAUNCHED();
+  return NVX_OK;
+}

@@ -37,6 +37,12 @@ _SIGS = {
                                    c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p,
                                    c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p,
                                    c_void_p], c_int32),
+    "nvx_rmsnorm": ([c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
+                     c_float, c_void_p], c_int32),
+    "nvx_qk_norm_rope": ([c_void_p, c_int64, c_int32, c_int32, c_int32, c_void_p, c_void_p,
+                          c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_float, c_void_p],
+                         c_int32),
+    "nvx_silu_mul": ([c_void_p, c_int64, c_void_p, c_int32, c_int32, c_void_p], c_int32),
     "nvx_timing_enable": ([c_int32], c_int32),
     "nvx_timing_read": ([c_int32, POINTER(c_double), POINTER(c_int64)], c_int32),
     "nvx_timing_reset": ([], c_int32),

@@ -3,13 +3,14 @@
 Mirrors the reference's nanovllm/models/qwen3.py:14-216 (module names, fused
 qkv_proj / gate_up_proj, q/k RMSNorm, NeoX RoPE, add+RMSNorm residual stream,
 ``compute_logits`` over every row).  Tensor parallelism is left out: one process
-drives one GPU.  Dense projections are torch (hipBLASLt) GEMMs; attention is
-``nanovllm.layers.attention.Attention`` on the HIP library.
+drives one GPU.  Dense projections are torch (hipBLASLt) GEMMs; attention,
+RMSNorm, q/k-norm + RoPE and SiLU-mul run on the HIP library.
 """
 import torch
-import torch.nn.functional as F
 from torch import nn
 
+from nanovllm import _C
+from nanovllm.layers.activation import SiluAndMul
 from nanovllm.layers.attention import Attention
 from nanovllm.layers.layernorm import RMSNorm
 from nanovllm.layers.rotary_embedding import get_rope
@@ -40,14 +41,25 @@ class Qwen3Attention(nn.Module):
 
     def forward(self, positions, hidden_states):
         qkv = self.qkv_proj(hidden_states)
-        q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
-        q = q.view(-1, self.num_heads, self.head_dim)
-        k = k.view(-1, self.num_kv_heads, self.head_dim)
-        v = v.view(-1, self.num_kv_heads, self.head_dim)
-        if not self.qkv_bias:
-            q = self.q_norm(q)
-            k = self.k_norm(k)
-        q, k = self.rotary_emb(positions, q, k)
+        v = qkv[:, self.q_size + self.kv_size:].view(-1, self.num_kv_heads, self.head_dim)
+        if not self.qkv_bias and self.head_dim == 128:
+            # q/k RMSNorm + RoPE in one pass (reference qwen3.py:82-85)
+            N = qkv.shape[0]
+            q = torch.empty(N, self.num_heads, self.head_dim, dtype=qkv.dtype, device=qkv.device)
+            k = torch.empty(N, self.num_kv_heads, self.head_dim, dtype=qkv.dtype, device=qkv.device)
+            _C.check(_C.lib().nvx_qk_norm_rope(
+                _C.ptr(qkv), qkv.stride(0), self.num_heads, self.num_kv_heads, self.head_dim,
+                _C.ptr(self.q_norm.weight), _C.ptr(self.k_norm.weight), _C.ptr(positions),
+                _C.ptr(self.rotary_emb.cos_sin_cache), N, _C.ptr(q), _C.ptr(k),
+                float(self.q_norm.eps), _C.stream_of(qkv)))
+        else:
+            q, k, _ = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
+            q = q.view(-1, self.num_heads, self.head_dim)
+            k = k.view(-1, self.num_kv_heads, self.head_dim)
+            if not self.qkv_bias:
+                q = self.q_norm(q)
+                k = self.k_norm(k)
+            q, k = self.rotary_emb(positions, q, k)
         o = self.attn(q, k, v)
         return self.o_proj(o.flatten(1, -1))
 
@@ -59,10 +71,10 @@ class Qwen3MLP(nn.Module):
         assert hidden_act == "silu"
         self.gate_up_proj = nn.Linear(hidden_size, 2 * intermediate_size, bias=False)
         self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
+        self.act_fn = SiluAndMul()
 
     def forward(self, x):
-        gate, up = self.gate_up_proj(x).chunk(2, -1)
-        return self.down_proj(F.silu(gate) * up)
+        return self.down_proj(self.act_fn(self.gate_up_proj(x)))
 
 
 class Qwen3DecoderLayer(nn.Module):
