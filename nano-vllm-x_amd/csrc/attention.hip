@@ -5,16 +5,20 @@
 // nodes (row r -> node r / G, head hk*G + r % G), so one staged K/V chunk serves
 // the whole GQA group.  Each wave owns 32 q rows.
 //
-// Per 64-key chunk the workgroup stages K and V row-major in LDS (plain 128-bit
-// stores).  Every wave computes S^T = K . Q^T with v_mfma_f32_32x32x16_bf16: lane l
-// then holds query row l%32 and 16 keys per 32-key tile, so the online-softmax row
-// max and row sum are in-lane plus one exchange with lane l^32.  P^T goes straight
-// from those registers into the B operand of O^T += V^T . P^T; the contraction slots
-// are relabelled to the keys the lane already holds, and the V^T A operand comes
-// from two ds_read_b64_tr_b16 (gfx950 LDS transpose reads) per MFMA.
+// K and V arrive in LDS by LDS-DMA (global_load_lds_dwordx4) in 64-key chunks,
+// four chunks in a ring.  Every wave computes S^T = K . Q^T with
+// v_mfma_f32_32x32x16_bf16: lane l then holds query row l%32 and 16 keys per
+// 32-key tile, so the online-softmax row max and row sum are in-lane plus one
+// exchange with lane l^32.  P^T goes straight from those registers into the B
+// operand of O^T += V^T . P^T; the contraction slots are relabelled to the keys the
+// lane already holds, and the V^T A operand comes from two ds_read_b64_tr_b16
+// (gfx950 LDS transpose reads) per MFMA.
 //
-// Pipeline: two register stages of global loads (chunks c+1 and c+2 in flight while
-// chunk c is computed) and two LDS buffers, one barrier per chunk.
+// Software pipeline per wave: step c issues the S MFMAs of chunk c+1 interleaved
+// with the exp / row-sum / bf16 packing of chunk c, then the P.V MFMAs of chunk c,
+// so the matrix cores and the VALU work at the same time inside one wave.  The
+// ring holds chunk c (V being read), c+1 (K being read) and c+2, c+3 (in flight);
+// one barrier per chunk.
 //
 // Masking: keys < context_len - q_len are visible to all rows; key base+m is
 // visible to node i iff bit m of its tree mask (or m <= i without a mask).
@@ -26,7 +30,6 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kKC = 64;                         // keys per staged chunk
-constexpr int kStages = 3;                      // LDS ring: chunk c computed, c+1 and c+2 in flight
 constexpr int kTileBytes = kKC * kD * 2;        // one K (or V) chunk: 64 rows x 256 B
 constexpr int kStageBytes = 2 * kTileBytes;     // K then V
 constexpr int kDmaPerChunk = kStageBytes / 1024;  // 1 KB per wave-wide 16-byte-per-lane load
@@ -36,7 +39,9 @@ constexpr int kMaxSplitPages = 512;             // block-table entries one KV sp
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+constexpr bf16x2 kOnes2 = {(__bf16)1.0f, (__bf16)1.0f};
 
 struct AttnParams {
   const uint16_t* q;
@@ -81,6 +86,11 @@ __device__ __forceinline__ void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
 
+// Bits [0, n) set, n clamped to [0, 64].
+__device__ __forceinline__ uint64_t low_bits64(int n) {
+  return n <= 0 ? 0ull : (n >= 64 ? ~0ull : (1ull << n) - 1ull);
+}
+
 __device__ __forceinline__ int remap_xcd(int phys, int n) {
   // Blocks are dispatched round-robin over the 8 XCDs; give each XCD a
   // contiguous range of logical ids so the blocks of one (seq, kv head), which
@@ -91,11 +101,14 @@ __device__ __forceinline__ int remap_xcd(int phys, int n) {
   return start + slot;
 }
 
-template <int W>
-__global__ __launch_bounds__(W * 64) void tree_attn_kernel(AttnParams p) {
-  constexpr int NT = W * 64;
+// Two waves per SIMD (at most 256 VGPR+AGPR each): one 8-wave workgroup, or two
+// 4-wave workgroups sharing a CU.
+template <int W, int STAGES>
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void tree_attn_kernel(AttnParams p) {
   constexpr int PER = kDmaPerChunk / W;  // LDS-DMA loads per wave per chunk
-  __shared__ __attribute__((aligned(1024))) uint8_t ring[kStages * kStageBytes];
+  static_assert(STAGES == 2 || STAGES == 4, "ring of 2 (one chunk in flight) or 4 stages");
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[STAGES * kStageBytes];
   __shared__ int32_t pages[kMaxSplitPages];
 
   const int logical = remap_xcd(blockIdx.x, gridDim.x);
@@ -117,26 +130,27 @@ __global__ __launch_bounds__(W * 64) void tree_attn_kernel(AttnParams p) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, g = lane >> 5, lr = lane & 31;
-  const int r = row0 + wave * 32 + lr;
+  const int r = row0 + wave * 32 + lr;  // this lane's q row
   const bool row_ok = r < rows_total;
+  const bool wave_active = row0 + wave * 32 < rows_total;
   const int node = row_ok ? r / p.G : 0;
   const int head = hk * p.G + (row_ok ? r % p.G : 0);
   const int token = q0 + node;
-  const bool wave_active = row0 + wave * 32 < rows_total;
 
   // Q^T fragments (B operand of S^T = K.Q^T): d = 16*s + 8*g + [0..7].
   bf16x8 bq[8];
   {
+    const bool ld = row_ok && token < p.total_q;
     const uint16_t* qrow = p.q + ((int64_t)token * p.Hq + head) * kD + 8 * g;
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       uint4 v = make_uint4(0, 0, 0, 0);
-      if (row_ok && token < p.total_q) v = *reinterpret_cast<const uint4*>(qrow + 16 * s);
+      if (ld) v = *reinterpret_cast<const uint4*>(qrow + 16 * s);
       bq[s] = __builtin_bit_cast(bf16x8, v);
     }
   }
-  const uint64_t mbits = (p.tree_mask && row_ok && token < p.total_q) ? p.tree_mask[token] : 0ull;
   const bool use_tree = p.tree_mask != nullptr;
+  const uint64_t mbits = (use_tree && row_ok && token < p.total_q) ? p.tree_mask[token] : 0ull;
 
   // Keys beyond the last node of this chunk's rows are masked for every row.
   const int last_node = min(qlen - 1, (row0 + W * 32 - 1) / p.G);
@@ -154,7 +168,7 @@ __global__ __launch_bounds__(W * 64) void tree_attn_kernel(AttnParams p) {
   // without touching the vector-memory counter the DMA pipeline waits on.
   const int page0 = (c0 * kKC) / bs;
   const int npages = c1 > c0 ? ((c1 * kKC - 1) / bs - page0 + 1) : 0;
-  for (int i = tid; i < npages; i += NT)
+  for (int i = tid; i < npages; i += W * 64)
     pages[i] = (page0 + i < p.bt_stride) ? bt[page0 + i] : -1;
   // Make every prologue global load (Q, mask, pages) complete here, before the
   // first LDS-DMA is queued behind them.
@@ -181,9 +195,10 @@ __global__ __launch_bounds__(W * 64) void tree_attn_kernel(AttnParams p) {
     lane_row[j] = row;
     lane_off[j] = (uint32_t)(hk * kD * 2 + seg * 16);
   }
-  auto issue_chunk = [&](int c, int st) {
+  auto issue_chunk = [&](int c) {
+    const int st = (c - c0) & (STAGES - 1);
     const int pos0 = c * kKC;
-    const int32_t blk = pages[pos0 / bs - page0];
+    const int32_t blk = __builtin_amdgcn_readfirstlane(pages[pos0 / bs - page0]);
     const int64_t tok0 = blk >= 0 ? (int64_t)blk * bs + pos0 % bs : 0;
     const char* kbase = reinterpret_cast<const char*>(p.k_cache) + tok0 * row_stride;
     const char* vbase = reinterpret_cast<const char*>(p.v_cache) + tok0 * row_stride;
@@ -204,120 +219,238 @@ __global__ __launch_bounds__(W * 64) void tree_attn_kernel(AttnParams p) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) oacc[dt][j] = 0.f;
 
-  // V^T operand addressing for the transpose reads: 16-lane group q = lane/16
-  // supplies rows (keys) 4*(q/2) + i/4 and d columns 16*(q%2) + 4*(i%4).
+  // LDS byte addresses.  With the swizzle, every read address is a per-lane base
+  // plus the stage offset, XORed with a per-slice constant, plus an immediate:
+  //  K fragment (tile kt, d-slice s): row kt*32 + lr, slot (2s + g) ^ swz(lr)
+  //    = ((stage + k_lane) ^ (s << 5)) + kt * 8192
+  //  V^T transpose read (group ks, d tile dt, half h): 16-lane group q = lane/16
+  //  supplies rows (keys) 16*ks + 8*h + 4*(q/2) + i/4 and d columns
+  //  dt*32 + 16*(q%2) + 4*(i%4), i.e.
+  //    = ((stage + kTileBytes + v_lane[h]) ^ (dt << 6)) + ks * 4096
+  // (swz depends on row % 16 only, so the row terms 32*kt and 16*ks are plain
+  // offsets, and the XORed bits never carry into the row or stage bits.)
+  const uint32_t k_lane = (uint32_t)(lr * 256 + ((g ^ swz(lr)) << 4));
   const int tq = lane >> 4, ti = lane & 15;
   const int tr_key = 4 * (tq >> 1) + (ti >> 2);
   const int tr_d = 16 * (tq & 1) + 4 * (ti & 3);
+  const uint32_t v_lane0 = (uint32_t)(tr_key * 256 + ((((tr_d >> 3) ^ swz(tr_key))) << 4) + (tr_d & 7) * 2);
+  const uint32_t v_lane1 =
+      (uint32_t)((tr_key + 8) * 256 + ((((tr_d >> 3) ^ swz(tr_key + 8))) << 4) + (tr_d & 7) * 2);
 
-  auto compute_chunk = [&](int st, int c) {
-    const uint16_t* kb = reinterpret_cast<const uint16_t*>(ring + st * kStageBytes);
-    const uint16_t* vb = reinterpret_cast<const uint16_t*>(ring + st * kStageBytes + kTileBytes);
-    // S^T tiles: keys kt*32 + (j/4)*8 + 4*g + j%4, query row lr.
-    f32x16 sacc[2];
+  // S^T tiles of the chunk in stage st: sacc[kt] element j holds key
+  // kt*32 + (j/4)*8 + 4*g + j%4 of query row lr.  s_pair(s) adds the products over
+  // d = 16*s .. 16*s+15.
+  auto s_pair = [&](uint32_t kb, int s, f32x16 (&sacc)[2]) {
+    const uint32_t a = kb ^ (uint32_t)(s << 5);
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
-      const int krow = kt * 32 + lr;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) sacc[kt][j] = 0.f;
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const int slot = (2 * s + g) ^ swz(krow);
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&kb[krow * kD + slot * 8]);
-        sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq[s], sacc[kt], 0, 0, 0);
-      }
+      const bf16x8 k = *reinterpret_cast<const bf16x8*>(ring + a + kt * 8192);
+      sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k, bq[s], sacc[kt], 0, 0, 0);
     }
-    // Mask, then take the row max.  Scores stay unscaled; the scale (times
-    // log2 e) is folded into the exponent below.
-    const int pos0 = c * kKC;
-    const bool need_mask = pos0 + kKC > base;  // tree keys or keys past context_len
-    float mloc = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        float sv = sacc[kt][j];
-        if (need_mask) {
-          const int key = pos0 + kt * 32 + (j >> 2) * 8 + 4 * g + (j & 3);
-          bool vis = key < ctxlen;
-          if (vis && key >= base) {
-            const int mm = key - base;
-            vis = use_tree ? (((mbits >> mm) & 1ull) != 0ull) : (mm <= node);
-          }
-          if (!vis) sv = -INFINITY;
-        }
-        sacc[kt][j] = sv;
-        mloc = fmaxf(mloc, sv);
-      }
-    }
-    mloc = fmaxf(mloc, nvx::shfl_xor_f(mloc, 32)) * p.scale_log2;
-    // The reference max only moves up when a row's max grows by more than 2^8:
-    // P then stays <= 256 (exact after the final 1/l), and the O rescale is rare.
-    const bool grow = mloc > m_run + 8.f;
-    if (__any(grow)) {
-      const float m_new = grow ? mloc : m_run;
-      const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
-      m_run = m_new;
-    }
-    const bool dead = (m_run == -INFINITY);
-    const float neg_m = dead ? 0.f : -m_run;
-    float lsum = 0.f;
+  };
+  auto s_zero = [&](f32x16 (&sacc)[2]) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][j], p.scale_log2, neg_m));
-        sacc[kt][j] = pv;
-        lsum += pv;
-      }
-    lsum += nvx::shfl_xor_f(lsum, 32);
-    l_run += lsum;
-
-    // P^T as B operand: slot (g, i) of k-step ks holds key 16*ks + (i/4)*8 + 4*g + i%4.
-    bf16x8 bp[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) bp[ks][i] = (__bf16)sacc[ks >> 1][(ks & 1) * 8 + i];
-
+      for (int j = 0; j < 16; ++j) sacc[kt][j] = 0.f;
+  };
+  // O^T += V^T . P^T for key group ks (keys 16*ks .. 16*ks+15); vb0 / vb1 are the
+  // stage's V tile base plus v_lane0 / v_lane1.
+  auto pv_group = [&](uint32_t vb0, uint32_t vb1, int ks, bf16x8 bp) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
-      const int d = dt * 32 + tr_d;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const int r0 = 16 * ks + tr_key, r1 = r0 + 8;
-        const uint16_t* a0 = &vb[r0 * kD + (((d >> 3) ^ swz(r0)) << 3) + (d & 7)];
-        const uint16_t* a1 = &vb[r1 * kD + (((d >> 3) ^ swz(r1)) << 3) + (d & 7)];
-        const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(a0));
-        const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(a1));
-        const bf16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bp[ks], oacc[dt], 0, 0, 0);
-      }
+      const uint32_t x = (uint32_t)(dt << 6);
+      const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(ring + ((vb0 ^ x) + ks * 4096)));
+      const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(ring + ((vb1 ^ x) + ks * 4096)));
+      const bf16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bp, oacc[dt], 0, 0, 0);
     }
   };
 
-  // Ring pipeline, one barrier per chunk: wait for chunk c's loads (chunk c+1's may
-  // still be in flight), barrier (also: every wave is done with chunk c-1, whose
-  // stage receives chunk c+2), issue chunk c+2, compute chunk c.
-  if (c0 < c1) issue_chunk(c0, 0);
-  if (c0 + 1 < c1) issue_chunk(c0 + 1, 1);
-  int st = 0;
-  for (int c = c0; c < c1; ++c) {
-    if (c + 1 < c1)
-      wait_vm<PER>();
-    else
+  // One step: the S MFMAs of chunk cs (in stage sts, into sdst; skipped when
+  // !kS), then the softmax (VALU) and P.V MFMAs of chunk c from scur.  With the
+  // 4-stage ring cs = c+1, so the S MFMAs of the next chunk never wait for this
+  // chunk's softmax; with the 2-stage ring cs = c and sdst is scur.
+  auto step = [&](auto s_tag, int c, int sts, f32x16 (&scur)[2], f32x16 (&sdst)[2]) {
+    constexpr bool kS = decltype(s_tag)::value;
+    const int st = (c - c0) & (STAGES - 1);
+    const uint32_t kb_s = (uint32_t)(sts * kStageBytes) + k_lane;
+    const uint32_t vb0 = (uint32_t)(st * kStageBytes + kTileBytes) + v_lane0;
+    const uint32_t vb1 = (uint32_t)(st * kStageBytes + kTileBytes) + v_lane1;
+    if (!wave_active) return;
+
+    auto phase_s = [&]() {
+      if constexpr (kS) {
+        s_zero(sdst);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) s_pair(kb_s, s, sdst);
+        // LDS reads run two d-slices ahead of the MFMAs that consume them.
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int i = 0; i < 6; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      }
+    };
+    // Probabilities of chunk c against the running reference max m_run, packed to
+    // bf16 for the P.V MFMAs; returns this lane's sum of the bf16 values (v_dot2
+    // with (1, 1), so numerator and denominator use the same rounded P).
+    bf16x8 bp[4];
+    auto probs = [&]() {
+      const float neg_m = (m_run == -INFINITY) ? 0.f : -m_run;
+      float lsum = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        // P^T as B operand: slot (g, i) of group ks holds key 16*ks + (i/4)*8 +
+        // 4*g + i%4, i.e. element (ks&1)*8 + i of scur[ks/2].
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          bp[ks][i] = (__bf16)__builtin_amdgcn_exp2f(
+              __builtin_fmaf(scur[ks >> 1][(ks & 1) * 8 + i], p.scale_log2, neg_m));
+        lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(bp[ks], bp[ks], 0, 1), kOnes2, lsum, false);
+        lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(bp[ks], bp[ks], 2, 3), kOnes2, lsum, false);
+        lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(bp[ks], bp[ks], 4, 5), kOnes2, lsum, false);
+        lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(bp[ks], bp[ks], 6, 7), kOnes2, lsum, false);
+      }
+      return lsum;
+    };
+    auto phase_softmax = [&]() {
+      const int pos0 = c * kKC;
+      if (pos0 + kKC > base) {  // tree keys or keys past context_len
+        // Visibility of the chunk's 64 keys for this row as one 64-bit word, cut at
+        // context_len.  Tree: keys before the tree, then the row's mask bits (a tree
+        // has at most 64 nodes).  Causal: keys up to base + node.  Element j of tile
+        // kt is key kt*32 + (j/4)*8 + 4*g + j%4.
+        const int off = base - pos0;  // chunk position of the first q-row key
+        uint64_t vis64;
+        if (use_tree)
+          vis64 = (off >= 0 ? (off >= 64 ? 0ull : mbits << off) : (off <= -64 ? 0ull : mbits >> -off)) |
+                  low_bits64(off);
+        else
+          vis64 = low_bits64(off + node + 1);
+        vis64 &= low_bits64(ctxlen - pos0);
+        const uint64_t v = vis64 >> (4 * g);
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int bit = kt * 32 + (j >> 2) * 8 + (j & 3);
+            scur[kt][j] = ((v >> bit) & 1ull) ? scur[kt][j] : -INFINITY;
+          }
+      }
+      // Speculative pass against the current reference max (scores stay unscaled;
+      // the scale times log2 e is folded into the exponent).  Each lane holds 16
+      // keys of its row; as long as their probabilities sum to <= 2^8 the reference
+      // stands (every P <= 2^8, exact after the final 1/l).  Otherwise -- a new
+      // maximum more than ~4-8 binary orders above the reference, an overflow, or
+      // the first visible keys of the row -- the exact row max of this chunk
+      // becomes the reference, O and l are rescaled, and P is recomputed.
+      float lsum = probs();
+      const bool redo = !(lsum <= 256.f) || m_run == -INFINITY;
+      if (__any(redo)) {
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) mloc = fmaxf(mloc, scur[kt][j]);
+        mloc = fmaxf(mloc, nvx::shfl_xor_f(mloc, 32)) * p.scale_log2;
+        const float m_new = fmaxf(m_run, mloc);
+        const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
+        m_run = m_new;
+        lsum = probs();
+      }
+      l_run += lsum;  // this lane's half of the row; the halves meet at the end
+    };
+    // MFMA phases run at raised wave priority: the wave that reaches the matrix
+    // core first keeps it for the whole phase while the other wave on the SIMD
+    // does its VALU phase.
+    __builtin_amdgcn_s_setprio(1);
+    phase_s();
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
+    phase_softmax();
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) pv_group(vb0, vb1, ks, bp[ks]);
+    // Transpose reads run two MFMAs ahead.
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 14; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  using Yes = std::true_type;
+  using No = std::false_type;
+  f32x16 sA[2], sB[2];
+  if constexpr (STAGES == 4) {
+    // Chunk c+1 must be resident before step c (c+2 may still be in flight); the
+    // barrier also retires every wave's reads of chunk c-1, whose stage then
+    // receives chunk c+3.
+    auto sync = [&](int c) {
+      if (c + 2 < c1)
+        wait_vm<PER>();
+      else
+        wait_vm<0>();
+      __syncthreads();
+      if (c + 3 < c1) issue_chunk(c + 3);
+    };
+    if (c0 < c1) {
+      issue_chunk(c0);
+      if (c0 + 1 < c1) issue_chunk(c0 + 1);
+      if (c0 + 2 < c1) issue_chunk(c0 + 2);
+      if (c0 + 2 < c1)
+        wait_vm<2 * PER>();
+      else if (c0 + 1 < c1)
+        wait_vm<PER>();
+      else
+        wait_vm<0>();
+      __syncthreads();
+      if (wave_active) {
+        s_zero(sA);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) s_pair(k_lane, s, sA);
+      }
+      // Two steps per iteration so the score buffers alternate without copies.
+      int c = c0;
+      for (; c + 2 < c1; c += 2) {
+        sync(c);
+        step(Yes{}, c, (c + 1 - c0) & 3, sA, sB);
+        sync(c + 1);
+        step(Yes{}, c + 1, (c + 2 - c0) & 3, sB, sA);
+      }
+      if (c + 1 < c1) {
+        sync(c);
+        step(Yes{}, c, (c + 1 - c0) & 3, sA, sB);
+        step(No{}, c + 1, 0, sB, sA);
+      } else {
+        step(No{}, c, 0, sA, sB);
+      }
+    }
+  } else {
+    // One chunk in flight: wait for chunk c, barrier (every wave is done with
+    // chunk c-1, whose stage receives chunk c+1), then compute chunk c.
+    if (c0 < c1) issue_chunk(c0);
+    for (int c = c0; c < c1; ++c) {
       wait_vm<0>();
-    __syncthreads();
-    if (c + 2 < c1) issue_chunk(c + 2, st == 0 ? 2 : st - 1);
-    if (wave_active) compute_chunk(st, c);
-    st = st == kStages - 1 ? 0 : st + 1;
+      __syncthreads();
+      if (c + 1 < c1) issue_chunk(c + 1);
+      step(Yes{}, c, (c - c0) & 1, sA, sA);
+    }
   }
 
+  l_run += nvx::shfl_xor_f(l_run, 32);  // both halves share m_run
   if (!row_ok || token >= p.total_q) return;
   const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
   if (p.nsplit == 1) {
@@ -370,18 +503,17 @@ __global__ __launch_bounds__(kD) void combine_kernel(const float* __restrict__ p
 }
 
 struct Plan {
-  int W, nq, nsplit;
+  int W, stages, nq, nsplit;
 };
 
 Plan make_plan(int num_seqs, int max_q, int max_ctx, int Hq, int Hkv) {
   const int G = Hq / Hkv;
   const int rows = G * (max_q > 0 ? max_q : 1);
-  // 4 or 8 waves: enough threads to keep two chunks of K/V loads in flight.
-  const int W = rows <= 128 ? 4 : 8;
   Plan pl;
-  pl.W = W;
-  pl.nq = (rows + W * 32 - 1) / (W * 32);
-  const int64_t waves = (int64_t)num_seqs * Hkv * pl.nq * W;
+  pl.W = 4;
+  pl.stages = 2;
+  pl.nq = (rows + pl.W * 32 - 1) / (pl.W * 32);
+  const int64_t waves = (int64_t)num_seqs * Hkv * pl.nq * pl.W;
   int ns = (int)((kTargetWaves + waves - 1) / (waves > 0 ? waves : 1));
   const int max_chunks = (max_ctx + kKC - 1) / kKC;
   const int cap = max(1, max_chunks / 2);
@@ -472,10 +604,14 @@ extern "C" int nvx_tree_attention(const void* q, void* o, const void* k_cache, c
   const int64_t nblocks = (int64_t)num_seqs * num_kv_heads * pl.nq * pl.nsplit;
   NVX_CHECK(nblocks < (1ll << 31), "tree_attention: grid too large");
   const dim3 grid((unsigned)nblocks);
-  if (pl.W == 4)
-    hipLaunchKernelGGL(tree_attn_kernel<4>, grid, dim3(256), 0, s, p);
+  if (pl.W == 4 && pl.stages == 2)
+    hipLaunchKernelGGL((tree_attn_kernel<4, 2>), grid, dim3(256), 0, s, p);
+  else if (pl.W == 4)
+    hipLaunchKernelGGL((tree_attn_kernel<4, 4>), grid, dim3(256), 0, s, p);
+  else if (pl.stages == 2)
+    hipLaunchKernelGGL((tree_attn_kernel<8, 2>), grid, dim3(512), 0, s, p);
   else
-    hipLaunchKernelGGL(tree_attn_kernel<8>, grid, dim3(512), 0, s, p);
+    hipLaunchKernelGGL((tree_attn_kernel<8, 4>), grid, dim3(512), 0, s, p);
   NVX_LAUNCHED();
   if (pl.nsplit > 1) {
     hipLaunchKernelGGL(combine_kernel, dim3(total_q * num_heads), dim3(kD), 0, s, p.part_o,
