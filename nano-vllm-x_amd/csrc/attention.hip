@@ -14,11 +14,11 @@
 // lane already holds, and the V^T A operand comes from two ds_read_b64_tr_b16
 // (gfx950 LDS transpose reads) per MFMA.
 //
-// Software pipeline per wave: step c issues the S MFMAs of chunk c+1 interleaved
-// with the exp / row-sum / bf16 packing of chunk c, then the P.V MFMAs of chunk c,
-// so the matrix cores and the VALU work at the same time inside one wave.  The
-// ring holds chunk c (V being read), c+1 (K being read) and c+2, c+3 (in flight);
-// one barrier per chunk.
+// Pipeline: a 2-stage LDS ring (64 KB), one chunk in flight while the other is
+// computed, one barrier per chunk.  A workgroup is 4 waves (one per SIMD) and
+// uses < 256 registers per wave, so two workgroups share a CU: each SIMD runs one
+// wave of each, and their independent MFMA and VALU phases (and prologues)
+// overlap.
 //
 // Masking: keys < context_len - q_len are visible to all rows; key base+m is
 // visible to node i iff bit m of its tree mask (or m <= i without a mask).
@@ -30,6 +30,7 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kKC = 64;                         // keys per staged chunk
+constexpr int kStages = 2;                      // LDS ring: chunk c computed, c+1 in flight
 constexpr int kTileBytes = kKC * kD * 2;        // one K (or V) chunk: 64 rows x 256 B
 constexpr int kStageBytes = 2 * kTileBytes;     // K then V
 constexpr int kDmaPerChunk = kStageBytes / 1024;  // 1 KB per wave-wide 16-byte-per-lane load
@@ -101,14 +102,12 @@ __device__ __forceinline__ int remap_xcd(int phys, int n) {
   return start + slot;
 }
 
-// Two waves per SIMD (at most 256 VGPR+AGPR each): one 8-wave workgroup, or two
-// 4-wave workgroups sharing a CU.
-template <int W, int STAGES>
+// Two waves per SIMD (at most 256 VGPR+AGPR each): two 4-wave workgroups per CU.
+template <int W>
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void tree_attn_kernel(AttnParams p) {
   constexpr int PER = kDmaPerChunk / W;  // LDS-DMA loads per wave per chunk
-  static_assert(STAGES == 2 || STAGES == 4, "ring of 2 (one chunk in flight) or 4 stages");
-  __shared__ __attribute__((aligned(1024))) uint8_t ring[STAGES * kStageBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[kStages * kStageBytes];
   __shared__ int32_t pages[kMaxSplitPages];
 
   const int logical = remap_xcd(blockIdx.x, gridDim.x);
@@ -196,7 +195,7 @@ void tree_attn_kernel(AttnParams p) {
     lane_off[j] = (uint32_t)(hk * kD * 2 + seg * 16);
   }
   auto issue_chunk = [&](int c) {
-    const int st = (c - c0) & (STAGES - 1);
+    const int st = (c - c0) & (kStages - 1);
     const int pos0 = c * kKC;
     const int32_t blk = __builtin_amdgcn_readfirstlane(pages[pos0 / bs - page0]);
     const int64_t tok0 = blk >= 0 ? (int64_t)blk * bs + pos0 % bs : 0;
@@ -267,32 +266,27 @@ void tree_attn_kernel(AttnParams p) {
     }
   };
 
-  // One step: the S MFMAs of chunk cs (in stage sts, into sdst; skipped when
-  // !kS), then the softmax (VALU) and P.V MFMAs of chunk c from scur.  With the
-  // 4-stage ring cs = c+1, so the S MFMAs of the next chunk never wait for this
-  // chunk's softmax; with the 2-stage ring cs = c and sdst is scur.
-  auto step = [&](auto s_tag, int c, int sts, f32x16 (&scur)[2], f32x16 (&sdst)[2]) {
-    constexpr bool kS = decltype(s_tag)::value;
-    const int st = (c - c0) & (STAGES - 1);
-    const uint32_t kb_s = (uint32_t)(sts * kStageBytes) + k_lane;
+  // One step on chunk c (in stage st): the S MFMAs into sacc, the softmax (VALU),
+  // then the P.V MFMAs.
+  auto step = [&](int c, f32x16 (&sacc)[2]) {
+    const int st = (c - c0) & (kStages - 1);
+    const uint32_t kb = (uint32_t)(st * kStageBytes) + k_lane;
     const uint32_t vb0 = (uint32_t)(st * kStageBytes + kTileBytes) + v_lane0;
     const uint32_t vb1 = (uint32_t)(st * kStageBytes + kTileBytes) + v_lane1;
     if (!wave_active) return;
 
     auto phase_s = [&]() {
-      if constexpr (kS) {
-        s_zero(sdst);
+      s_zero(sacc);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) s_pair(kb_s, s, sdst);
-        // LDS reads run two d-slices ahead of the MFMAs that consume them.
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      for (int s = 0; s < 8; ++s) s_pair(kb, s, sacc);
+      // LDS reads run a d-slice ahead of the MFMAs that consume them.
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-        for (int i = 0; i < 6; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      for (int i = 0; i < 6; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     };
     // Probabilities of chunk c against the running reference max m_run, packed to
     // bf16 for the P.V MFMAs; returns this lane's sum of the bf16 values (v_dot2
@@ -304,11 +298,11 @@ void tree_attn_kernel(AttnParams p) {
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         // P^T as B operand: slot (g, i) of group ks holds key 16*ks + (i/4)*8 +
-        // 4*g + i%4, i.e. element (ks&1)*8 + i of scur[ks/2].
+        // 4*g + i%4, i.e. element (ks&1)*8 + i of sacc[ks/2].
 #pragma unroll
         for (int i = 0; i < 8; ++i)
           bp[ks][i] = (__bf16)__builtin_amdgcn_exp2f(
-              __builtin_fmaf(scur[ks >> 1][(ks & 1) * 8 + i], p.scale_log2, neg_m));
+              __builtin_fmaf(sacc[ks >> 1][(ks & 1) * 8 + i], p.scale_log2, neg_m));
         lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(bp[ks], bp[ks], 0, 1), kOnes2, lsum, false);
         lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(bp[ks], bp[ks], 2, 3), kOnes2, lsum, false);
         lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(bp[ks], bp[ks], 4, 5), kOnes2, lsum, false);
@@ -337,7 +331,7 @@ void tree_attn_kernel(AttnParams p) {
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
             const int bit = kt * 32 + (j >> 2) * 8 + (j & 3);
-            scur[kt][j] = ((v >> bit) & 1ull) ? scur[kt][j] : -INFINITY;
+            sacc[kt][j] = ((v >> bit) & 1ull) ? sacc[kt][j] : -INFINITY;
           }
       }
       // Speculative pass against the current reference max (scores stay unscaled;
@@ -354,7 +348,7 @@ void tree_attn_kernel(AttnParams p) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-          for (int j = 0; j < 16; ++j) mloc = fmaxf(mloc, scur[kt][j]);
+          for (int j = 0; j < 16; ++j) mloc = fmaxf(mloc, sacc[kt][j]);
         mloc = fmaxf(mloc, nvx::shfl_xor_f(mloc, 32)) * p.scale_log2;
         const float m_new = fmaxf(m_run, mloc);
         const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -391,63 +385,15 @@ void tree_attn_kernel(AttnParams p) {
     __builtin_amdgcn_s_setprio(0);
   };
 
-  using Yes = std::true_type;
-  using No = std::false_type;
-  f32x16 sA[2], sB[2];
-  if constexpr (STAGES == 4) {
-    // Chunk c+1 must be resident before step c (c+2 may still be in flight); the
-    // barrier also retires every wave's reads of chunk c-1, whose stage then
-    // receives chunk c+3.
-    auto sync = [&](int c) {
-      if (c + 2 < c1)
-        wait_vm<PER>();
-      else
-        wait_vm<0>();
-      __syncthreads();
-      if (c + 3 < c1) issue_chunk(c + 3);
-    };
-    if (c0 < c1) {
-      issue_chunk(c0);
-      if (c0 + 1 < c1) issue_chunk(c0 + 1);
-      if (c0 + 2 < c1) issue_chunk(c0 + 2);
-      if (c0 + 2 < c1)
-        wait_vm<2 * PER>();
-      else if (c0 + 1 < c1)
-        wait_vm<PER>();
-      else
-        wait_vm<0>();
-      __syncthreads();
-      if (wave_active) {
-        s_zero(sA);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) s_pair(k_lane, s, sA);
-      }
-      // Two steps per iteration so the score buffers alternate without copies.
-      int c = c0;
-      for (; c + 2 < c1; c += 2) {
-        sync(c);
-        step(Yes{}, c, (c + 1 - c0) & 3, sA, sB);
-        sync(c + 1);
-        step(Yes{}, c + 1, (c + 2 - c0) & 3, sB, sA);
-      }
-      if (c + 1 < c1) {
-        sync(c);
-        step(Yes{}, c, (c + 1 - c0) & 3, sA, sB);
-        step(No{}, c + 1, 0, sB, sA);
-      } else {
-        step(No{}, c, 0, sA, sB);
-      }
-    }
-  } else {
-    // One chunk in flight: wait for chunk c, barrier (every wave is done with
-    // chunk c-1, whose stage receives chunk c+1), then compute chunk c.
-    if (c0 < c1) issue_chunk(c0);
-    for (int c = c0; c < c1; ++c) {
-      wait_vm<0>();
-      __syncthreads();
-      if (c + 1 < c1) issue_chunk(c + 1);
-      step(Yes{}, c, (c - c0) & 1, sA, sA);
-    }
+  // One chunk in flight: wait for chunk c, barrier (every wave is done with chunk
+  // c-1, whose stage receives chunk c+1), then compute chunk c.
+  f32x16 sacc[2];
+  if (c0 < c1) issue_chunk(c0);
+  for (int c = c0; c < c1; ++c) {
+    wait_vm<0>();
+    __syncthreads();
+    if (c + 1 < c1) issue_chunk(c + 1);
+    step(c, sacc);
   }
 
   l_run += nvx::shfl_xor_f(l_run, 32);  // both halves share m_run
@@ -503,17 +449,17 @@ __global__ __launch_bounds__(kD) void combine_kernel(const float* __restrict__ p
 }
 
 struct Plan {
-  int W, stages, nq, nsplit;
+  int nq, nsplit;
 };
+
+constexpr int kWaves = 4;  // waves per workgroup (32 q rows each)
 
 Plan make_plan(int num_seqs, int max_q, int max_ctx, int Hq, int Hkv) {
   const int G = Hq / Hkv;
   const int rows = G * (max_q > 0 ? max_q : 1);
   Plan pl;
-  pl.W = 4;
-  pl.stages = 2;
-  pl.nq = (rows + pl.W * 32 - 1) / (pl.W * 32);
-  const int64_t waves = (int64_t)num_seqs * Hkv * pl.nq * pl.W;
+  pl.nq = (rows + kWaves * 32 - 1) / (kWaves * 32);
+  const int64_t waves = (int64_t)num_seqs * Hkv * pl.nq * kWaves;
   int ns = (int)((kTargetWaves + waves - 1) / (waves > 0 ? waves : 1));
   const int max_chunks = (max_ctx + kKC - 1) / kKC;
   const int cap = max(1, max_chunks / 2);
@@ -604,14 +550,7 @@ extern "C" int nvx_tree_attention(const void* q, void* o, const void* k_cache, c
   const int64_t nblocks = (int64_t)num_seqs * num_kv_heads * pl.nq * pl.nsplit;
   NVX_CHECK(nblocks < (1ll << 31), "tree_attention: grid too large");
   const dim3 grid((unsigned)nblocks);
-  if (pl.W == 4 && pl.stages == 2)
-    hipLaunchKernelGGL((tree_attn_kernel<4, 2>), grid, dim3(256), 0, s, p);
-  else if (pl.W == 4)
-    hipLaunchKernelGGL((tree_attn_kernel<4, 4>), grid, dim3(256), 0, s, p);
-  else if (pl.stages == 2)
-    hipLaunchKernelGGL((tree_attn_kernel<8, 2>), grid, dim3(512), 0, s, p);
-  else
-    hipLaunchKernelGGL((tree_attn_kernel<8, 4>), grid, dim3(512), 0, s, p);
+  hipLaunchKernelGGL(tree_attn_kernel<kWaves>, grid, dim3(kWaves * 64), 0, s, p);
   NVX_LAUNCHED();
   if (pl.nsplit > 1) {
     hipLaunchKernelGGL(combine_kernel, dim3(total_q * num_heads), dim3(kD), 0, s, p.part_o,
