@@ -81,35 +81,64 @@ __global__ __launch_bounds__(kNormNT) void rmsnorm_kernel(const uint16_t* __rest
   }
 }
 
-// One wave per (token, head) of q and k; lane l owns elements l and l + 64, which
-// are exactly the pair NeoX RoPE rotates together (head_dim 128).
+// Eight lanes per (token, head) of q and k, 16-byte accesses: lane part p owns
+// elements 8p..8p+7 and 64+8p..64+8p+7 -- the pairs NeoX RoPE rotates together
+// (head_dim 128).  The head's sum of squares is reduced over the 8 lanes.
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const uint16_t* __restrict__ qkv, int64_t row_stride, int Hq, int Hkv,
     const uint16_t* __restrict__ qw, const uint16_t* __restrict__ kw,
     const int64_t* __restrict__ positions, const float* __restrict__ cos_sin, int N,
     uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_out, float eps) {
   const int H = Hq + Hkv;
-  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);  // global wave id
-  if (gw >= N * H) return;
-  const int lane = threadIdx.x & 63;
-  const int n = gw / H, h = gw % H;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t unit = t >> 3;  // (token, head)
+  const int part = (int)(t & 7);
+  // Units are whole 8-lane groups, so a group is either fully in range or fully out.
+  if (unit >= (int64_t)N * H) return;
+  const int n = (int)(unit / H), h = (int)(unit % H);
   const bool isq = h < Hq;
-  const uint16_t* src = qkv + (int64_t)n * row_stride + (int64_t)h * 128;
-  const float x1 = bf(src[lane]), x2 = bf(src[lane + 64]);
-  float ss = x1 * x1 + x2 * x2;
+  const uint16_t* src = qkv + (int64_t)n * row_stride + (int64_t)h * 128 + 8 * part;
+  const uint4 a = *reinterpret_cast<const uint4*>(src);
+  const uint4 b = *reinterpret_cast<const uint4*>(src + 64);
+  const uint16_t* ah = reinterpret_cast<const uint16_t*>(&a);
+  const uint16_t* bh = reinterpret_cast<const uint16_t*>(&b);
+  float x1[8], x2[8];
+  float ss = 0.f;
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) ss += nvx::shfl_xor_f(ss, off);
+  for (int e = 0; e < 8; ++e) {
+    x1[e] = bf(ah[e]);
+    x2[e] = bf(bh[e]);
+    ss += x1[e] * x1[e] + x2[e] * x2[e];
+  }
+#pragma unroll
+  for (int off = 1; off < 8; off <<= 1) ss += nvx::shfl_xor_f(ss, off);
   const float inv = rsqrtf(ss / 128.f + eps);
-  const uint16_t* w = isq ? qw : kw;
-  const float y1 = rbf(rbf(x1 * inv) * bf(w[lane]));
-  const float y2 = rbf(rbf(x2 * inv) * bf(w[lane + 64]));
-  const float* cs = cos_sin + positions[n] * 128;
-  const float c = cs[lane], s = cs[64 + lane];
-  const float o1 = y1 * c - y2 * s;
-  const float o2 = y2 * c + y1 * s;
-  uint16_t* dst = isq ? q_out + ((int64_t)n * Hq + h) * 128 : k_out + ((int64_t)n * Hkv + (h - Hq)) * 128;
-  dst[lane] = f2bf(o1);
-  dst[lane + 64] = f2bf(o2);
+  const uint16_t* w = (isq ? qw : kw) + 8 * part;
+  const uint4 wa = *reinterpret_cast<const uint4*>(w);
+  const uint4 wb = *reinterpret_cast<const uint4*>(w + 64);
+  const uint16_t* wah = reinterpret_cast<const uint16_t*>(&wa);
+  const uint16_t* wbh = reinterpret_cast<const uint16_t*>(&wb);
+  const float* cs = cos_sin + positions[n] * 128 + 8 * part;
+  const float4 c0 = *reinterpret_cast<const float4*>(cs);
+  const float4 c1 = *reinterpret_cast<const float4*>(cs + 4);
+  const float4 s0 = *reinterpret_cast<const float4*>(cs + 64);
+  const float4 s1 = *reinterpret_cast<const float4*>(cs + 68);
+  const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+  uint4 oa, ob;
+  uint16_t* oah = reinterpret_cast<uint16_t*>(&oa);
+  uint16_t* obh = reinterpret_cast<uint16_t*>(&ob);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float y1 = rbf(rbf(x1[e] * inv) * bf(wah[e]));
+    const float y2 = rbf(rbf(x2[e] * inv) * bf(wbh[e]));
+    oah[e] = f2bf(y1 * cv[e] - y2 * sv[e]);
+    obh[e] = f2bf(y2 * cv[e] + y1 * sv[e]);
+  }
+  uint16_t* dst = (isq ? q_out + ((int64_t)n * Hq + h) * 128 : k_out + ((int64_t)n * Hkv + (h - Hq)) * 128) +
+                  8 * part;
+  *reinterpret_cast<uint4*>(dst) = oa;
+  *reinterpret_cast<uint4*>(dst + 64) = ob;
 }
 
 // out[n, i] = bf16(silu(gate) * up), gate = gu[n, i], up = gu[n, I + i]; 8 per thread.
@@ -171,9 +200,12 @@ extern "C" int nvx_qk_norm_rope(const void* qkv, int64_t qkv_row_stride, int32_t
   if (num_tokens == 0) return NVX_OK;
   NVX_CHECK(qkv && q_norm_weight && k_norm_weight && positions && cos_sin_cache && q_out && k_out,
             "qk_norm_rope: null pointer");
-  const int64_t waves = (int64_t)num_tokens * (num_q_heads + num_kv_heads);
+  NVX_CHECK(a16(qkv) && a16(q_norm_weight) && a16(k_norm_weight) && a16(cos_sin_cache) &&
+                a16(q_out) && a16(k_out) && qkv_row_stride % 8 == 0,
+            "qk_norm_rope: pointers must be 16-byte aligned and the row stride a multiple of 8");
+  const int64_t lanes = (int64_t)num_tokens * (num_q_heads + num_kv_heads) * 8;
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s,
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, s,
                      (const uint16_t*)qkv, qkv_row_stride, num_q_heads, num_kv_heads,
                      (const uint16_t*)q_norm_weight, (const uint16_t*)k_norm_weight, positions,
                      cos_sin_cache, num_tokens, (uint16_t*)q_out, (uint16_t*)k_out, eps);
