@@ -22,17 +22,26 @@ class Config:
     eos: int = -1
     kvcache_block_size: int = 256
     num_kvcache_blocks: int = -1
-    # speculative decoding: "none" or "ngram"
+    # speculative decoding: "none", "ngram" or "eagle3".  For "eagle3",
+    # num_speculative_tokens is the number of tree nodes besides the root (T - 1).
     speculative_method: str = "none"
     num_speculative_tokens: int = 5
     ngram_max: int = 3
     ngram_min: int = 1
+    eagle_topk: int = 8
+    eagle_depth: int = 6
+    eagle_model: str = ""  # directory with the draft head's safetensors ("" = random init)
     seed: int = 0
 
     def __post_init__(self):
         assert self.kvcache_block_size % 256 == 0
         assert self.tensor_parallel_size == 1, "this build drives one GPU"
-        assert self.speculative_method in ("none", "ngram")
+        assert self.speculative_method in ("none", "ngram", "eagle3")
+        if self.speculative_method == "eagle3":
+            assert 1 + self.num_speculative_tokens <= 64, "a verify tree has at most 64 nodes"
+            assert self.eagle_topk * max(self.eagle_depth - 1, 1) <= 64
+            assert self.num_speculative_tokens <= self.eagle_topk + \
+                (self.eagle_depth - 1) * self.eagle_topk ** 2
         if self.hf_config is None:
             assert os.path.isdir(self.model)
             self.hf_config = AutoConfig.from_pretrained(self.model)
@@ -40,5 +49,11 @@ class Config:
 
     @property
     def verify_lookahead(self) -> int:
-        """KV positions a decode step writes per sequence (root + draft rows)."""
-        return 1 if self.speculative_method == "none" else 1 + self.num_speculative_tokens
+        """KV positions a decode step writes per sequence from len(seq)-1: the root and
+        draft rows of the verify tree, and for EAGLE-3 the draft head's expanded rows."""
+        if self.speculative_method == "none":
+            return 1
+        rows = 1 + self.num_speculative_tokens
+        if self.speculative_method == "eagle3":
+            rows = max(rows, self.eagle_topk * max(self.eagle_depth - 1, 1))
+        return rows

@@ -55,6 +55,9 @@ class LLMEngine:
             num_tokens = -sum(len(t) for t in token_ids)
         self.scheduler.postprocess(seqs, token_ids, is_prefill)
         outputs = [(seq.seq_id, seq.completion_token_ids) for seq in seqs if seq.is_finished]
+        for seq in seqs:
+            if seq.is_finished:
+                self.model_runner.drop_draft_state(seq.seq_id)
         return outputs, num_tokens
 
     def is_finished(self):

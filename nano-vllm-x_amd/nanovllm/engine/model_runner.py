@@ -17,6 +17,13 @@ a verify step:
    proposals); greedy sequences accept while the draft matches the argmax;
 4. the accepted tokens plus one recovered/bonus token go back to the scheduler.
 A chain's accepted path is already contiguous, so no compaction is needed.
+
+``speculative_method="eagle3"`` drafts with a one-layer EAGLE-3 head
+(nanovllm/models/eagle3.py) fed by the target's residual stream at three layers:
+the head catches up on every prefill chunk and on every verify step's accepted
+rows, expands a top-k tree (nanovllm/spec/eagle3.py), and the target verifies the
+tree (delta mode); the accepted path's target KV rows are then compacted
+(``nvx_kv_compact``).
 """
 import glob
 import os
@@ -27,7 +34,10 @@ import torch
 from nanovllm.config import Config
 from nanovllm.engine.sequence import Sequence
 from nanovllm.layers.sampler import RejectionSampler, Sampler
+from nanovllm.models.eagle3 import Eagle3DraftModel
 from nanovllm.models.qwen3 import Qwen3ForCausalLM, random_init_
+from nanovllm.spec.eagle3 import expand_tree, tree_depths, tree_masks
+from nanovllm.spec.kv_compact import kv_compact
 from nanovllm.spec.ngram import NgramProposer
 from nanovllm.spec.tree import ancestor_masks, chain_parents
 from nanovllm.utils.context import get_context, reset_context, set_context
@@ -52,6 +62,12 @@ class ModelRunner:
         torch.set_default_device("cuda")
         self.model = Qwen3ForCausalLM(hf_config)
         self.load_or_init(config.model)
+        self.draft = None
+        if config.speculative_method == "eagle3":
+            self.draft = Eagle3DraftModel(hf_config)
+            self.draft.bind_target(self.model)
+            self.load_or_init_draft(config.eagle_model)
+            self.draft_state = {}  # seq_id -> (feature [H], top-k tokens [k], top-k log-probs [k])
         self.sampler = Sampler()
         self.rejection = RejectionSampler()
         self.allocate_kv_cache()
@@ -62,6 +78,8 @@ class ModelRunner:
             self.proposer = NgramProposer(config.ngram_max, config.ngram_min,
                                           config.num_speculative_tokens)
         self.gen = torch.Generator(device="cuda").manual_seed(config.seed)
+        # verify-step statistics: steps per sequence and histogram of accepted draft tokens
+        self.spec_stats = {"verify_rows": 0, "accepted": 0, "accepted_hist": {}}
 
     def load_or_init(self, path):
         files = glob.glob(os.path.join(path, "*.safetensors")) if path and os.path.isdir(path) else []
@@ -91,6 +109,24 @@ class ModelRunner:
                         if name in params:
                             params[name].data.copy_(w)
 
+    def load_or_init_draft(self, path):
+        files = glob.glob(os.path.join(path, "*.safetensors")) if path and os.path.isdir(path) else []
+        if not files:
+            random_init_(self.draft, seed=self.config.seed + 1)
+            return
+        from safetensors import safe_open
+        params = dict(self.draft.named_parameters())
+        for f in files:
+            with safe_open(f, "pt", "cpu") as fh:
+                for name in fh.keys():
+                    key = name.replace("midlayer.", "")
+                    if key in params:
+                        params[key].data.copy_(fh.get_tensor(name))
+
+    def drop_draft_state(self, seq_id):
+        if self.draft is not None:
+            self.draft_state.pop(seq_id, None)
+
     def exit(self):
         torch.cuda.synchronize()
 
@@ -103,7 +139,8 @@ class ModelRunner:
         Hkv = hf.num_key_value_heads
         D = getattr(hf, "head_dim", hf.hidden_size // hf.num_attention_heads)
         dtype = torch.get_default_dtype()
-        block_bytes = 2 * hf.num_hidden_layers * self.block_size * Hkv * D * dtype.itemsize
+        layers = hf.num_hidden_layers + (1 if self.draft is not None else 0)
+        block_bytes = 2 * layers * self.block_size * Hkv * D * dtype.itemsize
         if config.num_kvcache_blocks <= 0:
             free, total = torch.cuda.mem_get_info()
             reserve = 8 << 30  # activations, logits and fp32 probabilities of a step
@@ -114,6 +151,11 @@ class ModelRunner:
         for l, attn in enumerate(self.model.attention_layers()):
             attn.k_cache = self.kv_cache[0, l]
             attn.v_cache = self.kv_cache[1, l]
+        if self.draft is not None:
+            # the draft head's one layer, paged with the target's block tables
+            self.draft_kv_cache = torch.empty(2, config.num_kvcache_blocks, self.block_size, Hkv, D)
+            attn = self.draft.attention_layers()[0]
+            attn.k_cache, attn.v_cache = self.draft_kv_cache[0], self.draft_kv_cache[1]
 
     def prepare_block_tables(self, seqs: list[Sequence]):
         max_len = max(len(seq.block_table) for seq in seqs)
@@ -182,6 +224,8 @@ class ModelRunner:
 
     @torch.inference_mode()
     def run(self, seqs: list[Sequence], is_prefill: bool):
+        if self.draft is not None:
+            return self.run_eagle_prefill(seqs) if is_prefill else self.run_eagle_verify(seqs)
         if is_prefill:
             input_ids, positions = self.prepare_prefill(seqs)
             temperatures = self.prepare_sample(seqs)
@@ -204,4 +248,143 @@ class ModelRunner:
         _, acc, out_tokens, _ = self.rejection(logits, temperatures, None, tokens, parents, U, Uf,
                                                num_nodes)
         acc, out_tokens = acc.tolist(), out_tokens.tolist()
+        self._count(acc)
         return [out_tokens[b][:acc[b] + 1] for b in range(B)]
+
+    def _count(self, acc):
+        st = self.spec_stats
+        st["verify_rows"] += len(acc)
+        st["accepted"] += sum(acc)
+        for a in acc:
+            st["accepted_hist"][a] = st["accepted_hist"].get(a, 0) + 1
+
+    # ---------------------------------------------------------------- EAGLE-3 ----
+
+    def _slots(self, seq, start, count):
+        bt = seq.block_table
+        return [bt[p // self.block_size] * self.block_size + p % self.block_size
+                for p in range(start, start + count)]
+
+    def _draft_state(self, normed, features, rows):
+        """Top-k of the next-token distribution after the given draft rows, and the
+        rows' output features (the state the next tree grows from)."""
+        k = self.config.eagle_topk
+        logp = torch.log_softmax(self.draft.compute_logits(normed[rows]).float(), dim=-1)
+        lp, tok = torch.topk(logp, k, dim=-1)
+        return features[rows], tok, lp
+
+    def run_eagle_prefill(self, seqs):
+        input_ids, positions = self.prepare_prefill(seqs)
+        temperatures = self.prepare_sample(seqs)
+        hidden, aux = self.model(input_ids, positions, self.draft.aux_layers)
+        cu = get_context().cu_seqlens_q
+        last = cu[1:].long() - 1
+        token_ids = self.sampler(self.model.compute_logits(hidden[last]), temperatures).tolist()
+        # Draft catch-up on the chunk: row q takes token q+1 (the sampled token after
+        # the prompt's last position) and the target feature at q.  Same attention
+        # context as the target's prefill (positions, slots, block tables).
+        shifted = []
+        for seq, tok in zip(seqs, token_ids):
+            start = seq.num_cached_tokens
+            end = start + seq.num_scheduled_tokens
+            nxt = seq[end] if end < seq.num_tokens else tok
+            shifted.extend(seq[start + 1:end] + [nxt])
+        normed, feats = self.draft(_pinned(shifted, torch.int64), positions, self.draft.fuse(aux))
+        done = [i for i, seq in enumerate(seqs)
+                if seq.num_cached_tokens + seq.num_scheduled_tokens == seq.num_tokens]
+        if done:
+            rows = last[torch.tensor(done, device=last.device)]
+            f, tok, lp = self._draft_state(normed, feats, rows)
+            for j, i in enumerate(done):
+                self.draft_state[seqs[i].seq_id] = (f[j], tok[j], lp[j])
+        reset_context()
+        return token_ids
+
+    def _eagle_tree(self, seqs, ctx, block_tables):
+        """Expand one draft tree per sequence; returns (tokens [B, T-1], parents [B, T])."""
+        cfg = self.config
+        k, depth, T = cfg.eagle_topk, cfg.eagle_depth, 1 + cfg.num_speculative_tokens
+        B = len(seqs)
+        states = [self.draft_state[seq.seq_id] for seq in seqs]
+        root_feat = torch.stack([s[0] for s in states])
+        root_tok = torch.stack([s[1] for s in states])
+        root_lp = torch.stack([s[2] for s in states])
+        rmax = k * max(depth - 1, 1)
+        slots = torch.tensor([self._slots(seq, c, rmax) for seq, c in zip(seqs, ctx)],
+                             dtype=torch.int32, pin_memory=True).cuda(non_blocking=True)
+        ctx_d = _pinned(ctx, torch.int64)
+        row_level = torch.arange(rmax, device="cuda") // k        # position offset of row r
+        H = root_feat.shape[-1]
+        max_ctx = max(ctx)
+
+        def draft_rows(rows_tok, rows_feat, rows_mask, level):
+            R = rows_tok.shape[1]
+            positions = (ctx_d.unsqueeze(1) + row_level[:R]).reshape(-1)
+            set_context(False, cu_seqlens_q=torch.arange(0, B * R + 1, R, dtype=torch.int32,
+                                                         device="cuda"),
+                        max_seqlen_q=R, slot_mapping=slots[:, :R].reshape(-1).contiguous(),
+                        context_lens=(ctx_d + R).to(torch.int32), block_tables=block_tables,
+                        tree_mask=rows_mask.reshape(-1).contiguous(), max_context_len=max_ctx + R)
+            normed, feats = self.draft(rows_tok.reshape(-1), positions, rows_feat.reshape(B * R, H))
+            reset_context()
+            last = normed.view(B, R, H)[:, R - k:].reshape(B * k, H)
+            logp = torch.log_softmax(self.draft.compute_logits(last).float(), dim=-1)
+            lp, tok = torch.topk(logp, k, dim=-1)
+            return (tok.view(B, k, k), lp.view(B, k, k)), feats.view(B, R, H)[:, R - k:]
+
+        return expand_tree(draft_rows, root_tok, root_lp, root_feat, depth, T)
+
+    def run_eagle_verify(self, seqs):
+        cfg = self.config
+        T = 1 + cfg.num_speculative_tokens
+        B = len(seqs)
+        ctx = [len(seq) - 1 for seq in seqs]
+        block_tables = self.prepare_block_tables(seqs)
+        tree_tok, parents = self._eagle_tree(seqs, ctx, block_tables)
+        # target verify of the trees: node i at position ctx + depth(i), stored at ctx + i
+        roots = _pinned([seq.last_token for seq in seqs], torch.int64)
+        tokens = torch.cat([roots.unsqueeze(1), tree_tok], dim=1)            # [B, T]
+        ctx_d = _pinned(ctx, torch.int64)
+        positions = (ctx_d.unsqueeze(1) + tree_depths(parents, cfg.eagle_depth)).reshape(-1)
+        slot_mapping = _pinned([sl for seq, c in zip(seqs, ctx) for sl in self._slots(seq, c, T)],
+                               torch.int32)
+        context_lens = (ctx_d + T).to(torch.int32)
+        set_context(False, cu_seqlens_q=torch.arange(0, B * T + 1, T, dtype=torch.int32, device="cuda"),
+                    max_seqlen_q=T, slot_mapping=slot_mapping, context_lens=context_lens,
+                    block_tables=block_tables,
+                    tree_mask=tree_masks(parents, cfg.eagle_depth).reshape(-1).contiguous(),
+                    max_context_len=max(ctx) + T)
+        hidden, aux = self.model(tokens.reshape(-1), positions, self.draft.aux_layers)
+        logits = self.model.compute_logits(hidden)
+        reset_context()
+        temperatures = self.prepare_sample(seqs)
+        U = torch.rand(B, T, device="cuda", generator=self.gen)
+        Uf = torch.rand(B, device="cuda", generator=self.gen)
+        tok32, par32 = tokens.to(torch.int32), parents.to(torch.int32)
+        path, acc, out_tokens, _ = self.rejection(logits, temperatures, None, tok32, par32, U, Uf)
+        ctx32 = ctx_d.to(torch.int32)
+        kv_compact(self.kv_cache[0], self.kv_cache[1], block_tables, ctx32, path, acc)
+        acc_h, out_h, path_h = acc.tolist(), out_tokens.tolist(), path.tolist()
+        self._count(acc_h)
+        result = [out_h[b][:acc_h[b] + 1] for b in range(B)]
+        # Draft catch-up: rows ctx .. ctx+a take the accepted tokens then the bonus /
+        # recovered token, with the target features of the accepted path's tree rows.
+        rows, ids, pos, slots, cu = [], [], [], [], [0]
+        for b, seq in enumerate(seqs):
+            a = acc_h[b]
+            rows.extend(b * T + path_h[b][j] for j in range(a + 1))
+            ids.extend(result[b])
+            pos.extend(range(ctx[b], ctx[b] + a + 1))
+            slots.extend(self._slots(seq, ctx[b], a + 1))
+            cu.append(cu[-1] + a + 1)
+        ctx_after = [c + a + 1 for c, a in zip(ctx, acc_h)]
+        set_context(True, _pinned(cu, torch.int32), None, max(a + 1 for a in acc_h), max(ctx_after),
+                    _pinned(slots, torch.int32), _pinned(ctx_after, torch.int32), block_tables)
+        feats_in = self.draft.fuse(aux[_pinned(rows, torch.int64)])
+        normed, feats = self.draft(_pinned(ids, torch.int64), _pinned(pos, torch.int64), feats_in)
+        reset_context()
+        last = torch.tensor(cu[1:], device="cuda") - 1
+        f, tok, lp = self._draft_state(normed, feats, last)
+        for b, seq in enumerate(seqs):
+            self.draft_state[seq.seq_id] = (f[b], tok[b], lp[b])
+        return result

@@ -1,0 +1,87 @@
+"""EAGLE-3 draft head for a Qwen3 target (Li et al., "EAGLE-3: Scaling up Inference
+Acceleration of Large Language Models via Training-Time Test", arXiv:2503.01840).
+
+The reference (nano-vllm 0.2.0) has no draft model.  The head is one decoder layer
+built from the target's own modules (nanovllm/models/qwen3.py:120-159 of the
+reference: attention with q/k norm and RoPE, SiLU MLP, add+RMSNorm residual stream):
+
+* the target's residual stream at three layers (low / middle / high) is fused by
+  ``fc`` (3*hidden -> hidden) into a feature g;
+* a draft row takes the embedding of one token and a feature,
+  ``x = [input_layernorm(embed(token)), hidden_norm(feature)]`` (2*hidden wide),
+  runs attention over x (the qkv projection is 2*hidden -> q+k+v), then the
+  post-attention add+RMSNorm and the MLP with the feature as the residual;
+* ``norm`` + ``lm_head`` give the next-token logits; the pre-norm sum is the row's
+  output feature, which feeds the draft's own next step (no ``fc``).
+
+Row convention (as in the public EAGLE-3 implementations): the draft row at
+position q takes token t[q+1] with the target feature at q and predicts t[q+2].
+The head attends over its own paged KV cache (one layer) through the same
+verify-path attention as the target, with the target's block tables.
+"""
+import torch
+from torch import nn
+
+from nanovllm.layers.layernorm import RMSNorm
+from nanovllm.models.qwen3 import Qwen3Attention, Qwen3MLP
+
+
+def default_aux_layers(num_layers):
+    """Target layers whose incoming residual stream forms the EAGLE-3 feature (low,
+    middle, high; clamped for very shallow targets)."""
+    last = num_layers - 1
+    return (min(2, last), min(num_layers // 2, last), max(0, num_layers - 3))
+
+
+class Eagle3DraftModel(nn.Module):
+
+    def __init__(self, config, aux_layers=None):
+        super().__init__()
+        H = config.hidden_size
+        self.aux_layers = tuple(aux_layers or default_aux_layers(config.num_hidden_layers))
+        self.fc = nn.Linear(len(self.aux_layers) * H, H, bias=False)
+        self.input_layernorm = RMSNorm(H, eps=config.rms_norm_eps)
+        self.hidden_norm = RMSNorm(H, eps=config.rms_norm_eps)
+        self.self_attn = Qwen3Attention(
+            hidden_size=H,
+            num_heads=config.num_attention_heads,
+            num_kv_heads=config.num_key_value_heads,
+            max_position=config.max_position_embeddings,
+            rms_norm_eps=config.rms_norm_eps,
+            qkv_bias=getattr(config, "attention_bias", False),
+            head_dim=getattr(config, "head_dim", None),
+            rope_theta=getattr(config, "rope_theta", None) or 1000000,
+            rope_scaling=getattr(config, "rope_scaling", None),
+            input_size=2 * H,
+        )
+        self.post_attention_layernorm = RMSNorm(H, eps=config.rms_norm_eps)
+        self.mlp = Qwen3MLP(H, config.intermediate_size, config.hidden_act)
+        self.norm = RMSNorm(H, eps=config.rms_norm_eps)
+        self.lm_head = nn.Linear(H, config.vocab_size, bias=False)
+        self.embed_tokens = None  # the target's embedding, bound by bind_target
+
+    def bind_target(self, target):
+        """Share the target's token embedding (not a parameter of the head)."""
+        object.__setattr__(self, "embed_tokens", target.model.embed_tokens)
+
+    def fuse(self, aux):
+        """Target residual streams [N, 3*H] -> feature [N, H]."""
+        return self.fc(aux)
+
+    def forward(self, input_ids, positions, features):
+        """One draft row per (token, feature).  Returns (logits-ready hidden [N, H],
+        output feature [N, H]); the attention context comes from the global Context
+        and the head's KV cache, as for the target's layers."""
+        emb = self.embed_tokens(input_ids)
+        x = torch.cat([self.input_layernorm(emb), self.hidden_norm(features)], dim=-1)
+        h = self.self_attn(positions, x)
+        h, residual = self.post_attention_layernorm(h, features)
+        h = self.mlp(h)
+        normed, out_feature = self.norm(h, residual)
+        return normed, out_feature
+
+    def compute_logits(self, hidden_states):
+        return self.lm_head(hidden_states)
+
+    def attention_layers(self):
+        return [self.self_attn.attn]

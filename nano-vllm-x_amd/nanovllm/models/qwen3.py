@@ -20,7 +20,7 @@ class Qwen3Attention(nn.Module):
 
     def __init__(self, hidden_size, num_heads, num_kv_heads, max_position=4096 * 32,
                  head_dim=None, rms_norm_eps=1e-06, qkv_bias=False, rope_theta=10000,
-                 rope_scaling=None):
+                 rope_scaling=None, input_size=None):
         super().__init__()
         self.num_heads = num_heads
         self.num_kv_heads = num_kv_heads
@@ -29,7 +29,9 @@ class Qwen3Attention(nn.Module):
         self.kv_size = self.num_kv_heads * self.head_dim
         self.scaling = self.head_dim ** -0.5
         self.qkv_bias = qkv_bias
-        self.qkv_proj = nn.Linear(hidden_size, self.q_size + 2 * self.kv_size, bias=qkv_bias)
+        # input_size: width of the attention input (2*hidden in an EAGLE-3 draft layer)
+        self.qkv_proj = nn.Linear(input_size or hidden_size, self.q_size + 2 * self.kv_size,
+                                  bias=qkv_bias)
         self.o_proj = nn.Linear(self.q_size, hidden_size, bias=False)
         if isinstance(rope_scaling, dict):
             rope_theta = rope_scaling.get("rope_theta", rope_theta)
@@ -96,11 +98,13 @@ class Qwen3DecoderLayer(nn.Module):
         self.input_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
         self.post_attention_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
 
-    def forward(self, positions, hidden_states, residual):
+    def forward(self, positions, hidden_states, residual, aux=None):
         if residual is None:
             hidden_states, residual = self.input_layernorm(hidden_states), hidden_states
         else:
             hidden_states, residual = self.input_layernorm(hidden_states, residual)
+        if aux is not None:  # the residual stream entering this layer
+            aux.append(residual)
         hidden_states = self.self_attn(positions, hidden_states)
         hidden_states, residual = self.post_attention_layernorm(hidden_states, residual)
         return self.mlp(hidden_states), residual
@@ -115,13 +119,21 @@ class Qwen3Model(nn.Module):
                                      for _ in range(config.num_hidden_layers)])
         self.norm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
 
-    def forward(self, input_ids, positions):
+    def forward(self, input_ids, positions, aux_layers=None):
+        """aux_layers: layer indices whose incoming residual stream is also returned
+        (concatenated, [N, len(aux_layers) * hidden]) -- the EAGLE-3 target features."""
         hidden_states = self.embed_tokens(input_ids)
         residual = None
-        for layer in self.layers:
-            hidden_states, residual = layer(positions, hidden_states, residual)
+        captured = {}
+        for i, layer in enumerate(self.layers):
+            aux = [] if aux_layers and i in aux_layers else None
+            hidden_states, residual = layer(positions, hidden_states, residual, aux)
+            if aux:
+                captured[i] = aux[0]
         hidden_states, _ = self.norm(hidden_states, residual)
-        return hidden_states
+        if not aux_layers:
+            return hidden_states
+        return hidden_states, torch.cat([captured[i] for i in aux_layers], dim=-1)
 
 
 class Qwen3ForCausalLM(nn.Module):
@@ -133,8 +145,8 @@ class Qwen3ForCausalLM(nn.Module):
         if getattr(config, "tie_word_embeddings", False):
             self.lm_head.weight = self.model.embed_tokens.weight
 
-    def forward(self, input_ids, positions):
-        return self.model(input_ids, positions)
+    def forward(self, input_ids, positions, aux_layers=None):
+        return self.model(input_ids, positions, aux_layers)
 
     def compute_logits(self, hidden_states):
         return self.lm_head(hidden_states)

@@ -11,13 +11,14 @@ from transformers import Qwen3Config
 
 from nanovllm import LLM, SamplingParams
 from nanovllm.engine.sequence import Sequence
+from nanovllm.spec.tree import depths
 from nanovllm.utils.context import reset_context
 
 
-def tiny_config():
-    cfg = Qwen3Config(hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+def tiny_config(vocab=512, layers=2):
+    cfg = Qwen3Config(hidden_size=512, intermediate_size=1024, num_hidden_layers=layers,
                       num_attention_heads=4, num_key_value_heads=2, head_dim=128,
-                      vocab_size=512, max_position_embeddings=4096, rms_norm_eps=1e-6,
+                      vocab_size=vocab, max_position_embeddings=4096, rms_norm_eps=1e-6,
                       tie_word_embeddings=False, attention_bias=False, hidden_act="silu")
     cfg.rope_theta = 1000000
     cfg.dtype = torch.bfloat16
@@ -96,3 +97,104 @@ def test_plain_decode_equals_argmax(dev):
     logits = full_logits(llm, p + out)
     agree = sum(int(logits[len(p) + j - 1].argmax()) == t for j, t in enumerate(out))
     assert agree >= 19
+
+
+def check_greedy_is_argmax(llm, ps, outs, n):
+    checked = mismatched = 0
+    for p, o in zip(ps, outs):
+        toks = o["token_ids"]
+        assert len(toks) == n
+        logits = full_logits(llm, p + toks)
+        for j, t in enumerate(toks):
+            row = logits[len(p) + j - 1]
+            top2 = torch.topk(row, 2).values
+            checked += 1
+            if int(row.argmax()) != t:
+                mismatched += 1
+                assert float(top2[0] - top2[1]) < 0.05, (j, t, int(row.argmax()))
+    assert mismatched <= checked // 50
+
+
+@pytest.mark.gpu
+def test_eagle3_speculative_greedy_is_target_argmax(dev):
+    """EAGLE-3 trees (top-8, depth 4, 16 nodes) on a 64-token vocabulary, where a
+    random draft head still hits the target's argmax often enough to accept
+    multi-token paths (tree compaction and the draft catch-up are exercised)."""
+    V = 64
+    llm = LLM("unused", hf_config=tiny_config(vocab=V, layers=6), num_kvcache_blocks=64,
+              speculative_method="eagle3", num_speculative_tokens=15, eagle_topk=8, eagle_depth=4,
+              max_num_batched_tokens=4096)
+    rng = np.random.default_rng(3)
+    ps = [rng.integers(0, V, size=n).tolist() for n in (30, 257, 100, 513)]
+    outs = llm.generate(ps, SamplingParams(temperature=0.0, max_tokens=40, ignore_eos=True),
+                        use_tqdm=False)
+    check_greedy_is_argmax(llm, ps, outs, 40)
+    assert not llm.model_runner.draft_state  # finished sequences drop their draft state
+    hist = llm.model_runner.spec_stats["accepted_hist"]
+    print("accepted-length histogram", dict(sorted(hist.items())), flush=True)
+    assert sum(n for a, n in hist.items() if a >= 1) >= 5
+
+
+def greedy_continuation(llm, ids, n):
+    ids = list(ids)
+    out = []
+    for _ in range(n):
+        g = int(full_logits(llm, ids)[-1].argmax())
+        out.append(g)
+        ids.append(g)
+    return out
+
+
+@pytest.mark.gpu
+def test_eagle3_deep_acceptance_is_lossless(dev):
+    """The draft trees are built as usual, then the target's own greedy continuation is
+    written onto an existing depth-3 branch of each tree (a non-chain path at BFS
+    positions), so verification accepts multi-token paths: tree KV compaction and the
+    draft head's multi-row catch-up must keep the output equal to plain greedy."""
+    V = 64
+    llm = LLM("unused", hf_config=tiny_config(vocab=V, layers=6), num_kvcache_blocks=96,
+              speculative_method="eagle3", num_speculative_tokens=15, eagle_topk=4, eagle_depth=4,
+              max_num_batched_tokens=4096)
+    runner = llm.model_runner
+    orig = runner._eagle_tree
+
+    def planted(seqs, ctx, block_tables):
+        toks, parents = orig(seqs, ctx, block_tables)
+        toks = toks.clone()
+        par = parents.cpu().numpy()
+        for b, seq in enumerate(seqs):
+            d = depths(par[b])
+            v = int(np.argmax(d >= 3)) if (d >= 3).any() else int(np.argmax(d))
+            path = []
+            while v > 0:
+                path.append(v)
+                v = int(par[b][v])
+            path.reverse()
+            for node, g in zip(path, greedy_continuation(llm, seq.token_ids, len(path))):
+                toks[b, node - 1] = g
+        return toks, parents
+
+    runner._eagle_tree = planted
+    rng = np.random.default_rng(5)
+    ps = [rng.integers(0, V, size=n).tolist() for n in (64, 300)]
+    outs = llm.generate(ps, SamplingParams(temperature=0.0, max_tokens=32, ignore_eos=True),
+                        use_tqdm=False)
+    check_greedy_is_argmax(llm, ps, outs, 32)
+    hist = runner.spec_stats["accepted_hist"]
+    print("accepted-length histogram", dict(sorted(hist.items())), flush=True)
+    assert sum(n for a, n in hist.items() if a >= 2) >= 4
+
+
+@pytest.mark.gpu
+def test_eagle3_sampling_runs(dev):
+    V = 64
+    llm = LLM("unused", hf_config=tiny_config(vocab=V, layers=6), num_kvcache_blocks=64,
+              speculative_method="eagle3", num_speculative_tokens=31, eagle_topk=8, eagle_depth=6,
+              max_num_batched_tokens=300)  # chunked prefill of the long prompt
+    rng = np.random.default_rng(4)
+    ps = [rng.integers(0, V, size=n).tolist() for n in (50, 700, 120)]
+    sps = [SamplingParams(temperature=t, max_tokens=30, ignore_eos=True) for t in (1.0, 0.0, 0.7)]
+    outs = llm.generate(ps, sps, use_tqdm=False)
+    assert [len(o["token_ids"]) for o in outs] == [30] * 3
+    assert all(0 <= t < V for o in outs for t in o["token_ids"])
+    check_greedy_is_argmax(llm, ps[1:2], outs[1:2], 30)
