@@ -11,6 +11,13 @@ tokens are synthetic (seeded).  value = verified tokens/s = sum over the timed
 steps of sum_b (accepted_len_b + 1) / elapsed.
 
 Prints one JSON line.  `--gpus N` with N > 1 exits: this build runs on one GPU.
+
+`--workload e2e` runs the offline engine benchmark instead, with the methodology
+of the reference's bench.py (256 requests, prompt token ids U[0, 10000] of length
+U[100, 1024], max_tokens U[100, 1024], temperature 0.6, ignore_eos, one warmup
+generate, wall-clock timing): Qwen3-0.6B architecture with random-init weights,
+drafting with a random-init EAGLE-3 head (T = 32 tree nodes) or without
+speculation (`--spec none`); value = output tokens/s.
 """
 import argparse
 import json
@@ -43,7 +50,66 @@ def parse():
                     help="sequences in the CPU-baseline sample (0 disables it)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device copy (HBM counter calibration)")
+    ap.add_argument("--workload", choices=("verify", "e2e"), default="verify")
+    ap.add_argument("--spec", choices=("eagle3", "ngram", "none"), default="eagle3",
+                    help="e2e: speculative method")
+    ap.add_argument("--e2e-seqs", type=int, default=256)
+    ap.add_argument("--e2e-max-in", type=int, default=1024)
+    ap.add_argument("--e2e-max-out", type=int, default=1024)
+    ap.add_argument("--eagle-topk", type=int, default=8)
+    ap.add_argument("--eagle-depth", type=int, default=6)
     return ap.parse_args()
+
+
+def run_e2e(args):
+    """Offline output throughput through LLM.generate (reference bench.py:9-28)."""
+    from random import randint, seed
+    import torch
+    from nanovllm import LLM, SamplingParams
+    from nanovllm.models.qwen3 import qwen3_config
+
+    seed(0)
+    cfg = qwen3_config("Qwen3-0.6B")
+    cfg.eos_token_id = -1
+    T = 32 if args.tree_nodes == 64 else args.tree_nodes  # config 5 default: 32-node trees
+    kw = {}
+    if args.spec == "eagle3":
+        kw = dict(speculative_method="eagle3", num_speculative_tokens=T - 1,
+                  eagle_topk=args.eagle_topk, eagle_depth=args.eagle_depth)
+    elif args.spec == "ngram":
+        kw = dict(speculative_method="ngram", num_speculative_tokens=5)
+    blocks = args.e2e_seqs * ((args.e2e_max_in + args.e2e_max_out + 64) // 256 + 2) + 64
+    llm = LLM("unused", hf_config=cfg, max_model_len=4096, num_kvcache_blocks=blocks,
+              seed=args.seed, **kw)
+    prompt_token_ids = [[randint(0, 10000) for _ in range(randint(100, args.e2e_max_in))]
+                        for _ in range(args.e2e_seqs)]
+    sampling_params = [SamplingParams(temperature=0.6, ignore_eos=True,
+                                      max_tokens=randint(100, args.e2e_max_out))
+                       for _ in range(args.e2e_seqs)]
+    llm.generate([[1, 2, 3, 4]], SamplingParams(max_tokens=8), use_tqdm=False)
+    stats = llm.model_runner.spec_stats
+    stats.update(verify_rows=0, accepted=0, accepted_hist={})
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    # the progress bar (stderr) only redraws; the reference runs without it
+    llm.generate(prompt_token_ids, sampling_params, use_tqdm=True)
+    torch.cuda.synchronize()
+    t = time.perf_counter() - t
+    total = sum(sp.max_tokens for sp in sampling_params)
+    out = {
+        "metric": "output tokens/s, offline generate (reference bench.py workload)",
+        "value": total / t, "unit": "tokens/s", "n_gpus": 1, "higher_is_better": True,
+        "elapsed_s": t, "output_tokens": total, "dtype": "bf16",
+        "data": "synthetic (random-init weights, random prompt token ids)",
+        "config": {"workload": "offline generate", "model": "Qwen3-0.6B-shape", "requests": args.e2e_seqs,
+                   "input_len": f"U[100,{args.e2e_max_in}]", "output_len": f"U[100,{args.e2e_max_out}]",
+                   "temperature": 0.6, "speculative": args.spec,
+                   **({"tree_nodes": T, "eagle_topk": args.eagle_topk, "eagle_depth": args.eagle_depth}
+                      if args.spec == "eagle3" else {})},
+        "mean_accepted_per_verify": stats["accepted"] / max(stats["verify_rows"], 1),
+        "verify_rows": stats["verify_rows"],
+    }
+    print(json.dumps(out), flush=True)
 
 
 def read_pmc_traffic():
@@ -223,6 +289,9 @@ def main():
         print(json.dumps({"error": "this build runs the verify path on one GPU; --gpus must be 1",
                           "n_gpus": args.gpus}), flush=True)
         sys.exit(2)
+    if args.workload == "e2e":
+        run_e2e(args)
+        return
     import torch
     from nanovllm import _C
 
