@@ -58,6 +58,8 @@ def parse():
     ap.add_argument("--e2e-max-out", type=int, default=1024)
     ap.add_argument("--eagle-topk", type=int, default=8)
     ap.add_argument("--eagle-depth", type=int, default=6)
+    ap.add_argument("--graphs", action="store_true",
+                    help="e2e: replay verify / decode steps from captured HIP graphs")
     return ap.parse_args()
 
 
@@ -80,7 +82,7 @@ def run_e2e(args):
         kw = dict(speculative_method="ngram", num_speculative_tokens=5)
     blocks = args.e2e_seqs * ((args.e2e_max_in + args.e2e_max_out + 64) // 256 + 2) + 64
     llm = LLM("unused", hf_config=cfg, max_model_len=4096, num_kvcache_blocks=blocks,
-              seed=args.seed, **kw)
+              seed=args.seed, enforce_eager=not args.graphs, **kw)
     prompt_token_ids = [[randint(0, 10000) for _ in range(randint(100, args.e2e_max_in))]
                         for _ in range(args.e2e_seqs)]
     sampling_params = [SamplingParams(temperature=0.6, ignore_eos=True,
@@ -103,7 +105,7 @@ def run_e2e(args):
         "data": "synthetic (random-init weights, random prompt token ids)",
         "config": {"workload": "offline generate", "model": "Qwen3-0.6B-shape", "requests": args.e2e_seqs,
                    "input_len": f"U[100,{args.e2e_max_in}]", "output_len": f"U[100,{args.e2e_max_out}]",
-                   "temperature": 0.6, "speculative": args.spec,
+                   "temperature": 0.6, "speculative": args.spec, "hip_graphs": args.graphs,
                    **({"tree_nodes": T, "eagle_topk": args.eagle_topk, "eagle_depth": args.eagle_depth}
                       if args.spec == "eagle3" else {})},
         "mean_accepted_per_verify": stats["accepted"] / max(stats["verify_rows"], 1),

@@ -53,7 +53,7 @@ class ModelRunner:
         self.config = config
         hf_config = config.hf_config
         self.block_size = config.kvcache_block_size
-        self.enforce_eager = True
+        self.enforce_eager = config.enforce_eager
         self.world_size = 1
         self.rank = rank
         torch.cuda.set_device(rank)
@@ -71,6 +71,9 @@ class ModelRunner:
         self.sampler = Sampler()
         self.rejection = RejectionSampler()
         self.allocate_kv_cache()
+        self.graphs = {}
+        if not self.enforce_eager:
+            self.capture_cudagraph()
         torch.set_default_device("cpu")
         torch.set_default_dtype(default_dtype)
         self.proposer = None
@@ -186,8 +189,11 @@ class ModelRunner:
         return _pinned(input_ids, torch.int64), _pinned(positions, torch.int64)
 
     def prepare_decode(self, seqs: list[Sequence], drafts=None):
-        """Rows per sequence: the root (last token) then its draft tokens (a chain)."""
+        """Rows per sequence: the root (last token) then its draft tokens (a chain),
+        padded to the longest draft (to the captured graph's rows when graphs are on)."""
         T = 1 + (max(len(d) for d in drafts) if drafts else 0)
+        if self.graphs and len(seqs) <= self.graph_bs[-1]:
+            T = self.graph_vars["T"]
         input_ids, positions, slot_mapping, context_lens, num_nodes = [], [], [], [], []
         for i, seq in enumerate(seqs):
             ctx = len(seq) - 1
@@ -216,11 +222,91 @@ class ModelRunner:
 
     @torch.inference_mode()
     def run_model(self, input_ids, positions, is_prefill):
+        if not is_prefill and self.graphs and input_ids.numel() <= self.graph_vars["rows"]:
+            return self.model.compute_logits(self.replay_graph(input_ids, positions))
         hidden = self.model(input_ids, positions)
         if is_prefill:  # logits of each sequence's last scheduled token only
             cu = get_context().cu_seqlens_q
             hidden = hidden[cu[1:].long() - 1]
         return self.model.compute_logits(hidden)
+
+    # ------------------------------------------------------------ HIP graphs ----
+    # Verify / decode steps replay a captured target forward (reference
+    # model_runner.py:222-257, there for q_len = 1).  A graph covers bs sequences of
+    # T rows each (T = the verify step's rows, padded), with static input and context
+    # buffers; the attention launch is sized for max_model_len, so any context up to
+    # it fits.  Batches are padded to the next captured size with empty sequences
+    # (context 0, slot -1: nothing stored, output rows 0).  The LM head and the
+    # sampler run outside the graph.
+
+    def _graph_rows(self):
+        cfg = self.config
+        if cfg.speculative_method == "eagle3":
+            return None  # the EAGLE-3 steps run eagerly
+        return cfg.verify_lookahead
+
+    @torch.inference_mode()
+    def capture_cudagraph(self):
+        T = self._graph_rows()
+        if T is None:
+            return
+        cfg, hf = self.config, self.config.hf_config
+        max_bs = min(cfg.max_num_seqs, 512)
+        max_blocks = (cfg.max_model_len + T + self.block_size - 1) // self.block_size
+        rows = max_bs * T
+        gv = dict(
+            rows=rows, T=T, max_blocks=max_blocks,
+            input_ids=torch.zeros(rows, dtype=torch.int64),
+            positions=torch.zeros(rows, dtype=torch.int64),
+            slot_mapping=torch.full((rows,), -1, dtype=torch.int32),
+            context_lens=torch.zeros(max_bs, dtype=torch.int32),
+            block_tables=torch.full((max_bs, max_blocks), -1, dtype=torch.int32),
+            cu_seqlens_q=torch.arange(0, rows + 1, T, dtype=torch.int32),
+            tree_mask=torch.from_numpy(np.tile(ancestor_masks(chain_parents(T)), max_bs)).cuda()
+            if T > 1 else None,
+            outputs=torch.zeros(rows, hf.hidden_size),
+        )
+        self.graph_vars = gv
+        self.graph_bs = [b for b in [1, 2, 4, 8] + list(range(16, max_bs + 1, 16)) if b <= max_bs]
+        pool = None
+        for bs in reversed(self.graph_bs):
+            n = bs * T
+            set_context(False, cu_seqlens_q=gv["cu_seqlens_q"][:bs + 1], max_seqlen_q=T,
+                        slot_mapping=gv["slot_mapping"][:n], context_lens=gv["context_lens"][:bs],
+                        block_tables=gv["block_tables"][:bs],
+                        tree_mask=None if T == 1 else gv["tree_mask"][:n],
+                        max_context_len=cfg.max_model_len)
+            gv["outputs"][:n] = self.model(gv["input_ids"][:n], gv["positions"][:n])  # warmup
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, pool):
+                gv["outputs"][:n] = self.model(gv["input_ids"][:n], gv["positions"][:n])
+            if pool is None:
+                pool = graph.pool()
+            self.graphs[bs] = graph
+            torch.cuda.synchronize()
+            reset_context()
+
+    def replay_graph(self, input_ids, positions):
+        ctx, gv = get_context(), self.graph_vars
+        bs = ctx.context_lens.numel()
+        n = input_ids.numel()
+        if n != bs * gv["T"]:
+            raise RuntimeError(f"replay_graph: {n} rows for {bs} sequences, graph rows per "
+                               f"sequence {gv['T']}")
+        g = next(b for b in self.graph_bs if b >= bs)
+        gv["input_ids"][:n] = input_ids
+        gv["positions"][:n] = positions
+        gv["slot_mapping"].fill_(-1)
+        gv["slot_mapping"][:n] = ctx.slot_mapping
+        gv["context_lens"].zero_()
+        gv["context_lens"][:bs] = ctx.context_lens
+        gv["block_tables"].fill_(-1)
+        bt = ctx.block_tables
+        gv["block_tables"][:bs, :bt.shape[1]] = bt
+        if gv["tree_mask"] is not None:
+            gv["tree_mask"][:n] = ctx.tree_mask
+        self.graphs[g].replay()
+        return gv["outputs"][:n]
 
     @torch.inference_mode()
     def run(self, seqs: list[Sequence], is_prefill: bool):

@@ -198,3 +198,52 @@ def test_eagle3_sampling_runs(dev):
     assert [len(o["token_ids"]) for o in outs] == [30] * 3
     assert all(0 <= t < V for o in outs for t in o["token_ids"])
     check_greedy_is_argmax(llm, ps[1:2], outs[1:2], 30)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("spec", ["none", "ngram"])
+def test_graph_generate_is_target_argmax(dev, spec):
+    """Verify / decode steps replayed from captured HIP graphs (padded batches)."""
+    kw = dict(speculative_method="ngram", num_speculative_tokens=5) if spec == "ngram" else {}
+    llm = LLM("unused", hf_config=tiny_config(), num_kvcache_blocks=64, enforce_eager=False,
+              max_num_seqs=32, max_model_len=2048, max_num_batched_tokens=4096, **kw)
+    assert llm.model_runner.graphs
+    ps = prompts()
+    outs = llm.generate(ps, SamplingParams(temperature=0.0, max_tokens=24, ignore_eos=True),
+                        use_tqdm=False)
+    check_greedy_is_argmax(llm, ps, outs, 24)
+
+
+@pytest.mark.gpu
+def test_graph_replays_are_stable(dev):
+    """Three replays of one padded batch, with eager forwards and synchronisations in
+    between: every replay is bit-identical to the first and matches eager execution
+    to bf16 accuracy."""
+    llm = LLM("unused", hf_config=tiny_config(), num_kvcache_blocks=64, enforce_eager=False,
+              max_num_seqs=32, max_model_len=2048, speculative_method="ngram",
+              num_speculative_tokens=3)
+    runner, bm = llm.model_runner, llm.scheduler.block_manager
+    rng = np.random.default_rng(7)
+    seqs = []
+    for n in (100, 300, 257):
+        seq = Sequence(rng.integers(0, 512, size=n).tolist())
+        bm.allocate(seq, 0)
+        bm.may_append(seq, 4)
+        seqs.append(seq)
+    drafts = [[1, 2, 3], [], [7]]
+    with torch.inference_mode():
+        outs = []
+        for rep in range(3):
+            input_ids, positions, T, _ = runner.prepare_decode(seqs, drafts)
+            eager = runner.model(input_ids, positions).float()
+            torch.cuda.synchronize()
+            graph = runner.replay_graph(input_ids, positions).float().clone()
+            torch.cuda.synchronize()
+            reset_context()
+            outs.append(graph)
+            assert T == 4
+            assert float((graph - eager).abs().max()) < 5e-2
+        for o in outs[1:]:
+            assert torch.equal(o, outs[0])
+    for seq in seqs:
+        bm.deallocate(seq)
