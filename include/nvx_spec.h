@@ -92,7 +92,8 @@ int nvx_kv_compact(void* k_cache, void* v_cache, int64_t layer_stride_bytes,
  *   q, o          bf16 [cu_seqlens_q[num_seqs], num_heads, 128]
  *   k/v_cache     bf16 [*, block_size, num_kv_heads, 128]   (model_runner.py:115)
  *   block_tables  int32 [num_seqs, block_table_stride]
- *   cu_seqlens_q  int32 [num_seqs + 1]      context_lens int32 [num_seqs] (includes q rows)
+ *   cu_seqlens_q  int32 [num_seqs + 1]      context_lens int32 [num_seqs] (includes q rows,
+ *                 each <= max_context_len, which sizes the launch)
  *   tree_mask     uint64 [total q rows] or NULL: bit m of row i's mask makes key
  *                 (context_len - q_len + m) visible; NULL = causal (m <= i).
  *                 With a mask, q_len <= 64.

@@ -157,7 +157,9 @@ void tree_attn_kernel(AttnParams p) {
   const int nchunks = (key_end + kKC - 1) / kKC;
   const int cps = (nchunks + p.nsplit - 1) / p.nsplit;
   const int c0 = split * cps;
-  const int c1 = min(nchunks, c0 + cps);
+  // A context longer than the max_context_len the launch was sized for would overrun
+  // the LDS page table: such keys are dropped rather than written out of bounds.
+  const int c1 = min(min(nchunks, c0 + cps), c0 + ((kMaxSplitPages - 1) * p.block_size) / kKC);
 
   const int32_t* bt = p.block_tables + (int64_t)b * p.bt_stride;
   const int bs = p.block_size;
