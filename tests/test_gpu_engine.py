@@ -229,9 +229,17 @@ def test_graph_replays_are_stable(dev):
         seq = Sequence(rng.integers(0, 512, size=n).tolist())
         bm.allocate(seq, 0)
         bm.may_append(seq, 4)
+        seq.num_cached_tokens = 0
+        seq.num_scheduled_tokens = n
         seqs.append(seq)
     drafts = [[1, 2, 3], [], [7]]
     with torch.inference_mode():
+        # prefill the prompts so every attended KV position holds the model's own keys
+        # (the cache is allocated uninitialised)
+        input_ids, positions = runner.prepare_prefill(seqs)
+        runner.model(input_ids, positions)
+        torch.cuda.synchronize()
+        reset_context()
         outs = []
         for rep in range(3):
             input_ids, positions, T, _ = runner.prepare_decode(seqs, drafts)
