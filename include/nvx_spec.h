@@ -183,11 +183,27 @@ int nvx_qk_norm_rope(const void* qkv, int64_t qkv_row_stride, int32_t num_q_head
 int nvx_silu_mul(const void* gate_up, int64_t row_stride, void* out, int32_t num_rows,
                  int32_t inter, void* stream);
 
+/* ------------------------------------------------------- draft-head top-k --
+ * Top-k of log_softmax(logits[r]) for every row, in one pass over the logits.
+ * No counterpart in the reference (nano-vllm has no draft model); it serves the
+ * EAGLE-2/3 draft-tree expansion (arXiv:2406.16858), replacing
+ * torch.log_softmax(logits.float()) followed by torch.topk.
+ *   logits   [num_rows, logits_row_stride] of logits_dtype (BF16 or F32), 16-byte
+ *            aligned; vocab and the stride are multiples of 8 (bf16) or 4 (fp32)
+ *   out_tokens    int32 [num_rows, k]  token ids, by descending log-probability,
+ *                 equal values ordered by the lower token id
+ *   out_logprobs  fp32  [num_rows, k]  (x - max) - ln(sum exp(x - max))
+ * Limits: 1 <= k <= min(64, vocab); rows free of NaN.
+ */
+int nvx_topk_logprobs(const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
+                      int32_t num_rows, int32_t vocab, int32_t k, int32_t* out_tokens,
+                      float* out_logprobs, void* stream);
+
 /* ------------------------------------------------------------------ timing --
  * Optional per-entry-point HIP-event timing on the launch stream (used by the
  * benchmark to measure kernel durations in its timed region).
  * kernel ids: 0 ngram, 1 store_kvcache, 2 kv_compact, 3 tree_attention,
- *             4 temperature_softmax, 5 rejection_sample_tree.
+ *             4 temperature_softmax, 5 rejection_sample_tree, 6 topk_logprobs.
  */
 #define NVX_TIMER_NGRAM 0
 #define NVX_TIMER_STORE_KV 1
@@ -195,7 +211,8 @@ int nvx_silu_mul(const void* gate_up, int64_t row_stride, void* out, int32_t num
 #define NVX_TIMER_TREE_ATTENTION 3
 #define NVX_TIMER_SOFTMAX 4
 #define NVX_TIMER_REJECTION 5
-#define NVX_TIMER_COUNT 6
+#define NVX_TIMER_TOPK 6
+#define NVX_TIMER_COUNT 7
 
 int nvx_timing_enable(int on);
 /* Synchronises the recorded events and returns the accumulated milliseconds and

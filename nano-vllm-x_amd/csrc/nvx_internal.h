@@ -51,6 +51,29 @@ __device__ __forceinline__ float shfl_xor_f(float v, int off) { return __shfl_xo
 __device__ __forceinline__ int shfl_xor_i(int v, int off) { return __shfl_xor(v, off, 64); }
 __device__ __forceinline__ float shfl_up_f(float v, int off) { return __shfl_up(v, off, 64); }
 
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Unpacking of one 16-byte vector of a row (8 bf16 or 4 fp32 values) to fp32.
+template <typename VT>
+struct VecTraits;
+template <>
+struct VecTraits<uint16_t> {  // bf16: 8 values per 16 bytes
+  static constexpr int kPer = 8;
+  __device__ static void expand(const uint4& w, float (&x)[8]) {
+    x[0] = bf16_lo(w.x); x[1] = bf16_hi(w.x); x[2] = bf16_lo(w.y); x[3] = bf16_hi(w.y);
+    x[4] = bf16_lo(w.z); x[5] = bf16_hi(w.z); x[6] = bf16_lo(w.w); x[7] = bf16_hi(w.w);
+  }
+};
+template <>
+struct VecTraits<float> {  // fp32: 4 values per 16 bytes
+  static constexpr int kPer = 4;
+  __device__ static void expand(const uint4& w, float (&x)[4]) {
+    x[0] = __uint_as_float(w.x); x[1] = __uint_as_float(w.y);
+    x[2] = __uint_as_float(w.z); x[3] = __uint_as_float(w.w);
+  }
+};
+
 // Canonical block sum: xor butterfly inside each wave (offsets 32..1), then an xor
 // butterfly over the wave totals (offsets NW/2..1).  Every thread gets the result.
 // `red` must hold at least NW floats.  The fp32 association order is part of the

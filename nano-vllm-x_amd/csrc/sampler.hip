@@ -24,8 +24,6 @@ constexpr int kNT = 1024;
 constexpr int kNW = kNT / nvx::kWave;
 constexpr int kMaxNodes = 64;
 
-__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 __device__ __forceinline__ float load_logit(const void* row, int i, int dtype) {
   if (dtype == NVX_DTYPE_F32) return reinterpret_cast<const float*>(row)[i];
@@ -43,31 +41,13 @@ __device__ __forceinline__ float load_logit(const void* row, int i, int dtype) {
 constexpr int kVecNT = 1024;
 constexpr int kUnroll = 4;
 
-template <typename VT>
-struct VecTraits;
-template <>
-struct VecTraits<uint16_t> {  // bf16: 8 values per 16 bytes
-  static constexpr int kPer = 8;
-  __device__ static void expand(const uint4& w, float (&x)[8]) {
-    x[0] = bf16_lo(w.x); x[1] = bf16_hi(w.x); x[2] = bf16_lo(w.y); x[3] = bf16_hi(w.y);
-    x[4] = bf16_lo(w.z); x[5] = bf16_hi(w.z); x[6] = bf16_lo(w.w); x[7] = bf16_hi(w.w);
-  }
-};
-template <>
-struct VecTraits<float> {  // fp32: 4 values per 16 bytes
-  static constexpr int kPer = 4;
-  __device__ static void expand(const uint4& w, float (&x)[4]) {
-    x[0] = __uint_as_float(w.x); x[1] = __uint_as_float(w.y);
-    x[2] = __uint_as_float(w.z); x[3] = __uint_as_float(w.w);
-  }
-};
 
 template <typename VT>
 __global__ __launch_bounds__(kVecNT) void softmax_vec_kernel(const VT* __restrict__ logits,
                                                              int64_t stride,
                                                              const float* __restrict__ temps,
                                                              float* __restrict__ probs, int V) {
-  using Tr = VecTraits<VT>;
+  using Tr = nvx::VecTraits<VT>;
   constexpr int P = Tr::kPer;
   __shared__ float red[kVecNT / nvx::kWave];
   const int row = blockIdx.x;

@@ -15,7 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libnvx_spec.so"
 
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 TIMER_NGRAM, TIMER_STORE_KV, TIMER_KV_COMPACT, TIMER_TREE_ATTENTION, TIMER_SOFTMAX, \
-    TIMER_REJECTION = range(6)
+    TIMER_REJECTION, TIMER_TOPK = range(7)
 
 _SIGS = {
     "nvx_version": ([], c_int32),
@@ -43,6 +43,8 @@ _SIGS = {
                           c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_float, c_void_p],
                          c_int32),
     "nvx_silu_mul": ([c_void_p, c_int64, c_void_p, c_int32, c_int32, c_void_p], c_int32),
+    "nvx_topk_logprobs": ([c_void_p, c_int32, c_int64, c_int32, c_int32, c_int32, c_void_p,
+                           c_void_p, c_void_p], c_int32),
     "nvx_timing_enable": ([c_int32], c_int32),
     "nvx_timing_read": ([c_int32, POINTER(c_double), POINTER(c_int64)], c_int32),
     "nvx_timing_reset": ([], c_int32),

@@ -15,7 +15,7 @@ CSRC = PKG_DIR.parent / "csrc"
 INCLUDE = PKG_DIR.parent.parent / "include"
 LIB_DIR = PKG_DIR / "_lib"
 LIB_PATH = LIB_DIR / "libnvx_spec.so"
-SOURCES = ["capi.hip", "ngram.hip", "kvcache.hip", "sampler.hip", "attention.hip", "fused.hip"]
+SOURCES = ["capi.hip", "ngram.hip", "kvcache.hip", "sampler.hip", "attention.hip", "fused.hip", "draft.hip"]
 ARCH = "gfx950"
 
 

@@ -33,7 +33,7 @@ import torch
 
 from nanovllm.config import Config
 from nanovllm.engine.sequence import Sequence
-from nanovllm.layers.sampler import RejectionSampler, Sampler
+from nanovllm.layers.sampler import RejectionSampler, Sampler, topk_logprobs
 from nanovllm.models.eagle3 import Eagle3DraftModel
 from nanovllm.models.qwen3 import Qwen3ForCausalLM, random_init_
 from nanovllm.spec.eagle3 import expand_tree, tree_depths, tree_masks
@@ -354,9 +354,7 @@ class ModelRunner:
     def _draft_state(self, normed, features, rows):
         """Top-k of the next-token distribution after the given draft rows, and the
         rows' output features (the state the next tree grows from)."""
-        k = self.config.eagle_topk
-        logp = torch.log_softmax(self.draft.compute_logits(normed[rows]).float(), dim=-1)
-        lp, tok = torch.topk(logp, k, dim=-1)
+        lp, tok = topk_logprobs(self.draft.compute_logits(normed[rows]), self.config.eagle_topk)
         return features[rows], tok, lp
 
     def run_eagle_prefill(self, seqs):
@@ -414,8 +412,7 @@ class ModelRunner:
             normed, feats = self.draft(rows_tok.reshape(-1), positions, rows_feat.reshape(B * R, H))
             reset_context()
             last = normed.view(B, R, H)[:, R - k:].reshape(B * k, H)
-            logp = torch.log_softmax(self.draft.compute_logits(last).float(), dim=-1)
-            lp, tok = torch.topk(logp, k, dim=-1)
+            lp, tok = topk_logprobs(self.draft.compute_logits(last), k)
             return (tok.view(B, k, k), lp.view(B, k, k)), feats.view(B, R, H)[:, R - k:]
 
         return expand_tree(draft_rows, root_tok, root_lp, root_feat, depth, T)

@@ -9,6 +9,8 @@
   which the reference forbids at sampling_params.py:11.
 * ``rejection_sample_tree`` / ``rejection_sample_chain`` / ``RejectionSampler`` --
   speculative verification of a draft tree / chain (absent in the reference).
+* ``topk_logprobs`` -- the k most likely tokens of ``log_softmax(logits)`` per row in
+  one pass (the draft head's tree expansion; absent in the reference).
 """
 import torch
 from torch import nn
@@ -34,6 +36,25 @@ def temperature_softmax(logits: torch.Tensor, temperatures: torch.Tensor, out=No
         _C.ptr(logits), _DTYPE_CODE[logits.dtype], logits.stride(0), _C.ptr(temperatures),
         _C.ptr(probs), N, V, _C.stream_of(logits)))
     return probs
+
+
+def topk_logprobs(logits: torch.Tensor, k: int):
+    """Top-k of ``log_softmax(logits.float())`` per row: returns (log-probs fp32
+    [N, k], tokens int64 [N, k]) in the order of ``torch.topk`` (descending; equal
+    values by the lower token id).  logits [N, V] bf16 or fp32 with unit stride in V,
+    16-byte aligned rows."""
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("topk_logprobs: logits must be [N, V] with unit stride in V")
+    if logits.dtype not in _DTYPE_CODE:
+        raise ValueError(f"topk_logprobs: unsupported logits dtype {logits.dtype}")
+    N, V = logits.shape
+    tok = torch.empty(N, k, dtype=torch.int32, device=logits.device)
+    lp = torch.empty(N, k, dtype=torch.float32, device=logits.device)
+    _C.require_cuda(logits)
+    _C.check(_C.lib().nvx_topk_logprobs(
+        _C.ptr(logits), _DTYPE_CODE[logits.dtype], logits.stride(0), N, V, k, _C.ptr(tok),
+        _C.ptr(lp), _C.stream_of(logits)))
+    return lp, tok.long()
 
 
 def _i32(t):

@@ -21,6 +21,8 @@ reference semantics that do exist and the published algorithm for the rest:
                    decode of nanovllm/layers/attention.py:72-74.
 * ``kvcache``   -- slot scatter (nanovllm/layers/attention.py:21-30) and accepted
                    path compaction.
+* ``draft``     -- the EAGLE draft head's top-k of log_softmax (no reference
+                   counterpart; EAGLE-2 tree expansion, arXiv:2406.16858).
 
 How each function is pinned (golden vectors, library cross-checks, closed forms,
 brute force) is listed in each module's docstring and exercised in ``tests/``.
