@@ -40,9 +40,7 @@ constexpr int kMaxSplitPages = 512;             // block-table entries one KV sp
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
-constexpr bf16x2 kOnes2 = {(__bf16)1.0f, (__bf16)1.0f};
 
 struct AttnParams {
   const uint16_t* q;
@@ -291,26 +289,29 @@ void tree_attn_kernel(AttnParams p) {
       __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     };
     // Probabilities of chunk c against the running reference max m_run, packed to
-    // bf16 for the P.V MFMAs; returns this lane's sum of the bf16 values (v_dot2
-    // with (1, 1), so numerator and denominator use the same rounded P).
+    // bf16 for the P.V MFMAs; returns this lane's fp32 sum of the probabilities.
+    // The sum uses plain fp32 adds: v_dot2 (the bf16 dot product) executes in the
+    // matrix pipe and serialises with the other wave's MFMAs on the SIMD.
     bf16x8 bp[4];
     auto probs = [&]() {
       const float neg_m = (m_run == -INFINITY) ? 0.f : -m_run;
-      float lsum = 0.f;
+      float l0 = 0.f, l1 = 0.f;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         // P^T as B operand: slot (g, i) of group ks holds key 16*ks + (i/4)*8 +
         // 4*g + i%4, i.e. element (ks&1)*8 + i of sacc[ks/2].
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-          bp[ks][i] = (__bf16)__builtin_amdgcn_exp2f(
+        for (int i = 0; i < 8; ++i) {
+          const float e = __builtin_amdgcn_exp2f(
               __builtin_fmaf(sacc[ks >> 1][(ks & 1) * 8 + i], p.scale_log2, neg_m));
-        lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(bp[ks], bp[ks], 0, 1), kOnes2, lsum, false);
-        lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(bp[ks], bp[ks], 2, 3), kOnes2, lsum, false);
-        lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(bp[ks], bp[ks], 4, 5), kOnes2, lsum, false);
-        lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(bp[ks], bp[ks], 6, 7), kOnes2, lsum, false);
+          bp[ks][i] = (__bf16)e;
+          if (i & 1)
+            l1 += e;
+          else
+            l0 += e;
+        }
       }
-      return lsum;
+      return l0 + l1;
     };
     auto phase_softmax = [&]() {
       const int pos0 = c * kKC;
