@@ -74,7 +74,9 @@ class ModelRunner:
         self.graphs = {}
         if not self.enforce_eager:
             self.capture_cudagraph()
-        torch.set_default_device("cpu")
+        # None, not "cpu": a device context left installed routes every later torch call
+        # through a Python TorchFunctionMode (the default device is the CPU either way).
+        torch.set_default_device(None)
         torch.set_default_dtype(default_dtype)
         self.proposer = None
         if config.speculative_method == "ngram":
@@ -237,12 +239,14 @@ class ModelRunner:
     # buffers; the attention launch is sized for max_model_len, so any context up to
     # it fits.  Batches are padded to the next captured size with empty sequences
     # (context 0, slot -1: nothing stored, output rows 0).  The LM head and the
-    # sampler run outside the graph.
+    # sampler run outside the graph.  With EAGLE-3 the graph is the target's tree
+    # verify (T = tree nodes) and also returns the aux residual streams the draft head
+    # fuses; the draft levels and the catch-up run eagerly.
 
     def _graph_rows(self):
         cfg = self.config
         if cfg.speculative_method == "eagle3":
-            return None  # the EAGLE-3 steps run eagerly
+            return 1 + cfg.num_speculative_tokens
         return cfg.verify_lookahead
 
     @torch.inference_mode()
@@ -251,8 +255,10 @@ class ModelRunner:
         if T is None:
             return
         cfg, hf = self.config, self.config.hf_config
+        aux_layers = self.draft.aux_layers if self.draft is not None else None
         max_bs = min(cfg.max_num_seqs, 512)
-        max_blocks = (cfg.max_model_len + T + self.block_size - 1) // self.block_size
+        reserve = max(T, cfg.verify_lookahead)  # slots a step may reserve past the context
+        max_blocks = (cfg.max_model_len + reserve + self.block_size - 1) // self.block_size
         rows = max_bs * T
         gv = dict(
             rows=rows, T=T, max_blocks=max_blocks,
@@ -265,6 +271,7 @@ class ModelRunner:
             tree_mask=torch.from_numpy(np.tile(ancestor_masks(chain_parents(T)), max_bs)).cuda()
             if T > 1 else None,
             outputs=torch.zeros(rows, hf.hidden_size),
+            aux=torch.zeros(rows, len(aux_layers) * hf.hidden_size) if aux_layers else None,
         )
         self.graph_vars = gv
         self.graph_bs = [b for b in [1, 2, 4, 8] + list(range(16, max_bs + 1, 16)) if b <= max_bs]
@@ -276,10 +283,18 @@ class ModelRunner:
                         block_tables=gv["block_tables"][:bs],
                         tree_mask=None if T == 1 else gv["tree_mask"][:n],
                         max_context_len=cfg.max_model_len)
-            gv["outputs"][:n] = self.model(gv["input_ids"][:n], gv["positions"][:n])  # warmup
+            def forward():
+                if aux_layers is None:
+                    gv["outputs"][:n] = self.model(gv["input_ids"][:n], gv["positions"][:n])
+                else:
+                    h, a = self.model(gv["input_ids"][:n], gv["positions"][:n], aux_layers)
+                    gv["outputs"][:n] = h
+                    gv["aux"][:n] = a
+
+            forward()  # warmup
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, pool):
-                gv["outputs"][:n] = self.model(gv["input_ids"][:n], gv["positions"][:n])
+                forward()
             if pool is None:
                 pool = graph.pool()
             self.graphs[bs] = graph
@@ -306,6 +321,8 @@ class ModelRunner:
         if gv["tree_mask"] is not None:
             gv["tree_mask"][:n] = ctx.tree_mask
         self.graphs[g].replay()
+        if gv["aux"] is not None:
+            return gv["outputs"][:n], gv["aux"][:n]
         return gv["outputs"][:n]
 
     @torch.inference_mode()
@@ -437,7 +454,10 @@ class ModelRunner:
                     block_tables=block_tables,
                     tree_mask=tree_masks(parents, cfg.eagle_depth).reshape(-1).contiguous(),
                     max_context_len=max(ctx) + T)
-        hidden, aux = self.model(tokens.reshape(-1), positions, self.draft.aux_layers)
+        if self.graphs and B <= self.graph_bs[-1]:
+            hidden, aux = self.replay_graph(tokens.reshape(-1), positions)
+        else:
+            hidden, aux = self.model(tokens.reshape(-1), positions, self.draft.aux_layers)
         logits = self.model.compute_logits(hidden)
         reset_context()
         temperatures = self.prepare_sample(seqs)

@@ -135,6 +135,25 @@ def test_eagle3_speculative_greedy_is_target_argmax(dev):
     assert sum(n for a, n in hist.items() if a >= 1) >= 5
 
 
+@pytest.mark.gpu
+def test_eagle3_graph_verify_greedy_is_target_argmax(dev):
+    """The target's tree verify (with the aux residual streams) replayed from captured
+    HIP graphs, batches padded to the graph sizes: still the target's argmax."""
+    V = 64
+    llm = LLM("unused", hf_config=tiny_config(vocab=V, layers=6), num_kvcache_blocks=64,
+              speculative_method="eagle3", num_speculative_tokens=15, eagle_topk=8, eagle_depth=4,
+              max_num_batched_tokens=4096, enforce_eager=False, max_num_seqs=16,
+              max_model_len=2048)
+    assert llm.model_runner.graphs and llm.model_runner.graph_vars["T"] == 16
+    rng = np.random.default_rng(3)
+    ps = [rng.integers(0, V, size=n).tolist() for n in (30, 257, 100)]
+    outs = llm.generate(ps, SamplingParams(temperature=0.0, max_tokens=40, ignore_eos=True),
+                        use_tqdm=False)
+    check_greedy_is_argmax(llm, ps, outs, 40)
+    hist = llm.model_runner.spec_stats["accepted_hist"]
+    print("accepted-length histogram", dict(sorted(hist.items())), flush=True)
+
+
 def greedy_continuation(llm, ids, n):
     ids = list(ids)
     out = []
