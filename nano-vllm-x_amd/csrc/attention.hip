@@ -5,11 +5,12 @@
 // nodes (row r -> node r / G, head hk*G + r % G), so one staged K/V chunk serves
 // the whole GQA group.  Each wave owns 32 q rows.
 //
-// K and V arrive in LDS by LDS-DMA (global_load_lds_dwordx4) in 64-key chunks,
-// four chunks in a ring.  Every wave computes S^T = K . Q^T with
+// K and V arrive in LDS by LDS-DMA (global_load_lds_dwordx4) in 64-key chunks.
+// Every wave computes S^T = K . Q^T with
 // v_mfma_f32_32x32x16_bf16: lane l then holds query row l%32 and 16 keys per
 // 32-key tile, so the online-softmax row max and row sum are in-lane plus one
-// exchange with lane l^32.  P^T goes straight from those registers into the B
+// exchange with lane l^32 (the row max only when the reference max is redone; the
+// row sums once, at the end).  P^T goes straight from those registers into the B
 // operand of O^T += V^T . P^T; the contraction slots are relabelled to the keys the
 // lane already holds, and the V^T A operand comes from two ds_read_b64_tr_b16
 // (gfx950 LDS transpose reads) per MFMA.
