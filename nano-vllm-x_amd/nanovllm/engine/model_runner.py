@@ -81,7 +81,8 @@ class ModelRunner:
         self.proposer = None
         if config.speculative_method == "ngram":
             self.proposer = NgramProposer(config.ngram_max, config.ngram_min,
-                                          config.num_speculative_tokens)
+                                          config.num_speculative_tokens,
+                                          capacity=config.max_model_len + config.verify_lookahead)
         self.gen = torch.Generator(device="cuda").manual_seed(config.seed)
         # verify-step statistics: steps per sequence and histogram of accepted draft tokens
         self.spec_stats = {"verify_rows": 0, "accepted": 0, "accepted_hist": {}}
@@ -131,6 +132,8 @@ class ModelRunner:
     def drop_draft_state(self, seq_id):
         if self.draft is not None:
             self.draft_state.pop(seq_id, None)
+        if self.proposer is not None:
+            self.proposer.drop(seq_id)
 
     def exit(self):
         torch.cuda.synchronize()
@@ -336,7 +339,9 @@ class ModelRunner:
             token_ids = self.sampler(logits, temperatures).tolist()
             reset_context()
             return token_ids
-        drafts = self.proposer.propose([seq.token_ids for seq in seqs]) if self.proposer else None
+        drafts = (self.proposer.propose_seqs([seq.seq_id for seq in seqs],
+                                             [seq.token_ids for seq in seqs])
+                  if self.proposer else None)
         input_ids, positions, T, num_nodes = self.prepare_decode(seqs, drafts)
         temperatures = self.prepare_sample(seqs)
         logits = self.run_model(input_ids, positions, False)

@@ -51,3 +51,27 @@ def test_proposer_lists(dev):
     prop = NgramProposer(3, 1, 5)
     h = [1, 2, 3, 4, 5, 9, 1, 2, 3]
     assert prop.propose([h, [8]]) == [[4, 5, 9, 1, 2], []]
+
+
+@pytest.mark.gpu
+def test_proposer_resident_histories_match_packed(dev):
+    """propose_seqs (device-resident histories, only appended tokens copied) equals
+    propose (every history packed) over growing histories, with rows dropped and
+    reused and the resident buffer grown past its first size."""
+    rng = np.random.default_rng(11)
+    res = NgramProposer(3, 1, 5, capacity=600)
+    ref = NgramProposer(3, 1, 5)
+    hist = {k: rng.integers(0, 40, size=int(rng.integers(1, 200))).tolist() for k in range(90)}
+    for step in range(6):
+        keys = sorted(hist)
+        got = res.propose_seqs(keys, [hist[k] for k in keys])
+        assert got == ref.propose([hist[k] for k in keys]), step
+        for k in keys:  # accept up to one draft token plus a new one
+            hist[k] += (got[keys.index(k)][:1] + rng.integers(0, 40, size=1).tolist())
+        for k in keys[step::7]:  # finished sequences leave; new ones arrive
+            res.drop(k)
+            del hist[k]
+        for j in range(5):
+            hist[1000 * (step + 1) + j] = rng.integers(0, 40, size=int(rng.integers(1, 300))).tolist()
+    with pytest.raises(ValueError, match="capacity"):
+        res.propose_seqs([-1], [[1] * 601])
