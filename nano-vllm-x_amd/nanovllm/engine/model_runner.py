@@ -198,7 +198,7 @@ class ModelRunner:
         padded to the longest draft (to the captured graph's rows when graphs are on)."""
         T = 1 + (max(len(d) for d in drafts) if drafts else 0)
         if self.graphs and len(seqs) <= self.graph_bs[-1]:
-            T = self.graph_vars["T"]
+            T = min(t for t in self.graph_vars if t >= T)
         input_ids, positions, slot_mapping, context_lens, num_nodes = [], [], [], [], []
         for i, seq in enumerate(seqs):
             ctx = len(seq) - 1
@@ -227,7 +227,7 @@ class ModelRunner:
 
     @torch.inference_mode()
     def run_model(self, input_ids, positions, is_prefill):
-        if not is_prefill and self.graphs and input_ids.numel() <= self.graph_vars["rows"]:
+        if not is_prefill and self._graph_fits(input_ids.numel()):
             return self.model.compute_logits(self.replay_graph(input_ids, positions))
         hidden = self.model(input_ids, positions)
         if is_prefill:  # logits of each sequence's last scheduled token only
@@ -238,8 +238,8 @@ class ModelRunner:
     # ------------------------------------------------------------ HIP graphs ----
     # Verify / decode steps replay a captured target forward (reference
     # model_runner.py:222-257, there for q_len = 1).  A graph covers bs sequences of
-    # T rows each (T = the verify step's rows, padded), with static input and context
-    # buffers; the attention launch is sized for max_model_len, so any context up to
+    # T rows each (T = 1 or the longest verify chain, a step using the smallest that
+    # fits its drafts), with static input and context buffers per T; the attention launch is sized for max_model_len, so any context up to
     # it fits.  Batches are padded to the next captured size with empty sequences
     # (context 0, slot -1: nothing stored, output rows 0).  The LM head and the
     # sampler run outside the graph.  With EAGLE-3 the graph is the target's tree
@@ -247,19 +247,33 @@ class ModelRunner:
     # fuses; the draft levels and the catch-up run eagerly.
 
     def _graph_rows(self):
+        """Rows per sequence of the captured graphs: the EAGLE-3 tree, or both a plain
+        decode row and the longest verify chain (a step replays the smallest that fits)."""
         cfg = self.config
         if cfg.speculative_method == "eagle3":
-            return 1 + cfg.num_speculative_tokens
-        return cfg.verify_lookahead
+            return [1 + cfg.num_speculative_tokens]
+        return sorted({1, cfg.verify_lookahead})
+
+    def _graph_fits(self, rows):
+        ctx = get_context()
+        if not self.graphs or ctx.context_lens is None:
+            return False
+        bs = ctx.context_lens.numel()
+        return 0 < bs <= self.graph_bs[-1] and rows % bs == 0 and rows // bs in self.graph_vars
 
     @torch.inference_mode()
     def capture_cudagraph(self):
-        T = self._graph_rows()
-        if T is None:
-            return
+        cfg = self.config
+        max_bs = min(cfg.max_num_seqs, 512)
+        self.graph_bs = [b for b in [1, 2, 4, 8] + list(range(16, max_bs + 1, 16)) if b <= max_bs]
+        self.graph_vars = {}
+        pool = None
+        for T in sorted(self._graph_rows(), reverse=True):
+            pool = self._capture_rows(T, max_bs, pool)
+
+    def _capture_rows(self, T, max_bs, pool):
         cfg, hf = self.config, self.config.hf_config
         aux_layers = self.draft.aux_layers if self.draft is not None else None
-        max_bs = min(cfg.max_num_seqs, 512)
         reserve = max(T, cfg.verify_lookahead)  # slots a step may reserve past the context
         max_blocks = (cfg.max_model_len + reserve + self.block_size - 1) // self.block_size
         rows = max_bs * T
@@ -276,9 +290,7 @@ class ModelRunner:
             outputs=torch.zeros(rows, hf.hidden_size),
             aux=torch.zeros(rows, len(aux_layers) * hf.hidden_size) if aux_layers else None,
         )
-        self.graph_vars = gv
-        self.graph_bs = [b for b in [1, 2, 4, 8] + list(range(16, max_bs + 1, 16)) if b <= max_bs]
-        pool = None
+        self.graph_vars[T] = gv
         for bs in reversed(self.graph_bs):
             n = bs * T
             set_context(False, cu_seqlens_q=gv["cu_seqlens_q"][:bs + 1], max_seqlen_q=T,
@@ -300,17 +312,19 @@ class ModelRunner:
                 forward()
             if pool is None:
                 pool = graph.pool()
-            self.graphs[bs] = graph
+            self.graphs[(T, bs)] = graph
             torch.cuda.synchronize()
             reset_context()
+        return pool
 
     def replay_graph(self, input_ids, positions):
-        ctx, gv = get_context(), self.graph_vars
+        ctx = get_context()
         bs = ctx.context_lens.numel()
         n = input_ids.numel()
-        if n != bs * gv["T"]:
-            raise RuntimeError(f"replay_graph: {n} rows for {bs} sequences, graph rows per "
-                               f"sequence {gv['T']}")
+        if not self._graph_fits(n):
+            raise RuntimeError(f"replay_graph: no captured graph for {n} rows of {bs} sequences "
+                               f"(rows per sequence {sorted(self.graph_vars)})")
+        gv = self.graph_vars[n // bs]
         g = next(b for b in self.graph_bs if b >= bs)
         gv["input_ids"][:n] = input_ids
         gv["positions"][:n] = positions
@@ -323,7 +337,7 @@ class ModelRunner:
         gv["block_tables"][:bs, :bt.shape[1]] = bt
         if gv["tree_mask"] is not None:
             gv["tree_mask"][:n] = ctx.tree_mask
-        self.graphs[g].replay()
+        self.graphs[(gv["T"], g)].replay()
         if gv["aux"] is not None:
             return gv["outputs"][:n], gv["aux"][:n]
         return gv["outputs"][:n]

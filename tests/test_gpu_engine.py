@@ -144,7 +144,7 @@ def test_eagle3_graph_verify_greedy_is_target_argmax(dev):
               speculative_method="eagle3", num_speculative_tokens=15, eagle_topk=8, eagle_depth=4,
               max_num_batched_tokens=4096, enforce_eager=False, max_num_seqs=16,
               max_model_len=2048)
-    assert llm.model_runner.graphs and llm.model_runner.graph_vars["T"] == 16
+    assert llm.model_runner.graphs and list(llm.model_runner.graph_vars) == [16]
     rng = np.random.default_rng(3)
     ps = [rng.integers(0, V, size=n).tolist() for n in (30, 257, 100)]
     outs = llm.generate(ps, SamplingParams(temperature=0.0, max_tokens=40, ignore_eos=True),
@@ -227,6 +227,7 @@ def test_graph_generate_is_target_argmax(dev, spec):
     llm = LLM("unused", hf_config=tiny_config(), num_kvcache_blocks=64, enforce_eager=False,
               max_num_seqs=32, max_model_len=2048, max_num_batched_tokens=4096, **kw)
     assert llm.model_runner.graphs
+    assert sorted(llm.model_runner.graph_vars) == ([1, 6] if spec == "ngram" else [1])
     ps = prompts()
     outs = llm.generate(ps, SamplingParams(temperature=0.0, max_tokens=24, ignore_eos=True),
                         use_tqdm=False)
