@@ -10,7 +10,7 @@ Qwen3-8B architecture; the cached context K/V, trees, draft distributions and
 tokens are synthetic (seeded).  value = verified tokens/s = sum over the timed
 steps of sum_b (accepted_len_b + 1) / elapsed.
 
-Prints one JSON line.  `--gpus N` with N > 1 exits: this build runs on one GPU.
+Prints one JSON line.  `--gpus N` with N > 1 exits: the verify path runs on a single GPU.
 
 `--workload e2e` runs the offline engine benchmark instead, with the methodology
 of the reference's bench.py (256 requests, prompt token ids U[0, 10000] of length
@@ -288,7 +288,7 @@ def cpu_baseline(args, torch, state, nseq):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs the verify path on one GPU; --gpus must be 1",
+        print(json.dumps({"error": "the verify path runs on a single GPU; --gpus must be 1",
                           "n_gpus": args.gpus}), flush=True)
         sys.exit(2)
     if args.workload == "e2e":

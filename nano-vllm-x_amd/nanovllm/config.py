@@ -35,7 +35,7 @@ class Config:
 
     def __post_init__(self):
         assert self.kvcache_block_size % 256 == 0
-        assert self.tensor_parallel_size == 1, "this build drives one GPU"
+        assert self.tensor_parallel_size == 1, "the verify path runs on a single GPU (tensor_parallel_size 1)"
         assert self.speculative_method in ("none", "ngram", "eagle3")
         if self.speculative_method == "eagle3":
             assert 1 + self.num_speculative_tokens <= 64, "a verify tree has at most 64 nodes"

@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product (the ``nanovllm`` package under
 ``nano-vllm-x_amd/`` or its HIP library) imports this package.  It is used by
-``tests/``, ``__graft_entry__.smoke()`` (as the checker) and ``bench.py``'s
+``tests/``, ``__graft_entry__.smoke()`` (to check the GPU results) and ``bench.py``'s
 ``cpu_baseline`` leg (as the timed CPU restatement).
 
 The reference (nano-vllm 0.2.0) has no drafter, tree attention, rejection sampler

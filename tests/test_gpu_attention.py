@@ -3,7 +3,7 @@ import numpy as np
 import pytest
 import torch
 
-from nanovllm.layers.attention import store_kvcache, tree_attention, Attention
+from nanovllm.layers.attention import tree_attention, Attention
 from nanovllm.spec.tree import chain_parents, random_tree
 from nanovllm.utils.context import set_context, reset_context
 from nanovllm.utils.synthetic import VerifyBatch, randn_bf16
