@@ -35,7 +35,7 @@ constexpr int kStages = 2;                      // LDS ring: chunk c computed, c
 constexpr int kTileBytes = kKC * kD * 2;        // one K (or V) chunk: 64 rows x 256 B
 constexpr int kStageBytes = 2 * kTileBytes;     // K then V
 constexpr int kDmaPerChunk = kStageBytes / 1024;  // 1 KB per wave-wide 16-byte-per-lane load
-constexpr int kTargetWaves = 256 * 16;
+constexpr int kTargetWaves = 256 * 2 * 4;       // split-KV target: one round of two 4-wave workgroups per CU
 constexpr int kMaxSplitPages = 512;             // block-table entries one KV split may touch
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
