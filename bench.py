@@ -106,7 +106,8 @@ def run_e2e(args):
         "config": {"workload": "offline generate", "model": "Qwen3-0.6B-shape", "requests": args.e2e_seqs,
                    "input_len": f"U[100,{args.e2e_max_in}]", "output_len": f"U[100,{args.e2e_max_out}]",
                    "temperature": 0.6, "speculative": args.spec, "hip_graphs": args.graphs,
-                   **({"tree_nodes": T, "eagle_topk": args.eagle_topk, "eagle_depth": args.eagle_depth}
+                   **({"tree_nodes": T, "eagle_topk": args.eagle_topk, "eagle_depth": args.eagle_depth,
+                       "draft_vocab": llm.model_runner.draft.lm_head.weight.shape[0]}
                       if args.spec == "eagle3" else {})},
         "mean_accepted_per_verify": stats["accepted"] / max(stats["verify_rows"], 1),
         "verify_rows": stats["verify_rows"],

@@ -31,6 +31,9 @@ class Config:
     eagle_topk: int = 8
     eagle_depth: int = 6
     eagle_model: str = ""  # directory with the draft head's safetensors ("" = random init)
+    # draft-head vocabulary for a random head (a checkpoint's config.json
+    # draft_vocab_size wins); 0 = the target vocabulary
+    eagle_draft_vocab: int = 32000
     seed: int = 0
 
     def __post_init__(self):

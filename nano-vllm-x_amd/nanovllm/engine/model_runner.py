@@ -64,7 +64,7 @@ class ModelRunner:
         self.load_or_init(config.model)
         self.draft = None
         if config.speculative_method == "eagle3":
-            self.draft = Eagle3DraftModel(hf_config)
+            self.draft = Eagle3DraftModel(hf_config, draft_vocab=self._draft_vocab(config))
             self.draft.bind_target(self.model)
             self.load_or_init_draft(config.eagle_model)
             self.draft_state = {}  # seq_id -> (feature [H], top-k tokens [k], top-k log-probs [k])
@@ -115,6 +115,18 @@ class ModelRunner:
                         if name in params:
                             params[name].data.copy_(w)
 
+    @staticmethod
+    def _draft_vocab(config):
+        """Draft-head vocabulary: the checkpoint's draft_vocab_size, else the config's."""
+        path = os.path.join(config.eagle_model, "config.json") if config.eagle_model else ""
+        if path and os.path.isfile(path):
+            import json
+            with open(path) as f:
+                n = json.load(f).get("draft_vocab_size")
+            if n:
+                return int(n)
+        return config.eagle_draft_vocab or None
+
     def load_or_init_draft(self, path):
         files = glob.glob(os.path.join(path, "*.safetensors")) if path and os.path.isdir(path) else []
         if not files:
@@ -122,12 +134,15 @@ class ModelRunner:
             return
         from safetensors import safe_open
         params = dict(self.draft.named_parameters())
+        buffers = dict(self.draft.named_buffers())
         for f in files:
             with safe_open(f, "pt", "cpu") as fh:
                 for name in fh.keys():
                     key = name.replace("midlayer.", "")
                     if key in params:
                         params[key].data.copy_(fh.get_tensor(name))
+                    elif key == "d2t":
+                        buffers["d2t"].copy_(fh.get_tensor(name))
 
     def drop_draft_state(self, seq_id):
         if self.draft is not None:
@@ -391,7 +406,7 @@ class ModelRunner:
         """Top-k of the next-token distribution after the given draft rows, and the
         rows' output features (the state the next tree grows from)."""
         lp, tok = topk_logprobs(self.draft.compute_logits(normed[rows]), self.config.eagle_topk)
-        return features[rows], tok, lp
+        return features[rows], self.draft.to_target(tok), lp
 
     def run_eagle_prefill(self, seqs):
         input_ids, positions = self.prepare_prefill(seqs)
@@ -449,6 +464,7 @@ class ModelRunner:
             reset_context()
             last = normed.view(B, R, H)[:, R - k:].reshape(B * k, H)
             lp, tok = topk_logprobs(self.draft.compute_logits(last), k)
+            tok = self.draft.to_target(tok)
             return (tok.view(B, k, k), lp.view(B, k, k)), feats.view(B, R, H)[:, R - k:]
 
         return expand_tree(draft_rows, root_tok, root_lp, root_feat, depth, T)

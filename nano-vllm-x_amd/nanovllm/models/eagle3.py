@@ -13,6 +13,9 @@ reference: attention with q/k norm and RoPE, SiLU MLP, add+RMSNorm residual stre
   post-attention add+RMSNorm and the MLP with the feature as the residual;
 * ``norm`` + ``lm_head`` give the next-token logits; the pre-norm sum is the row's
   output feature, which feeds the draft's own next step (no ``fc``).
+* the LM head covers a draft vocabulary (``draft_vocab`` ids, 32000 in the published
+  EAGLE-3 heads) and ``d2t`` maps a draft id to its target id (target = id + d2t[id],
+  the checkpoints' convention); a random head maps draft id i to target id i.
 
 Row convention (as in the public EAGLE-3 implementations): the draft row at
 position q takes token t[q+1] with the target feature at q and predicts t[q+2].
@@ -35,9 +38,10 @@ def default_aux_layers(num_layers):
 
 class Eagle3DraftModel(nn.Module):
 
-    def __init__(self, config, aux_layers=None):
+    def __init__(self, config, aux_layers=None, draft_vocab=None):
         super().__init__()
         H = config.hidden_size
+        draft_vocab = min(draft_vocab or config.vocab_size, config.vocab_size)
         self.aux_layers = tuple(aux_layers or default_aux_layers(config.num_hidden_layers))
         self.fc = nn.Linear(len(self.aux_layers) * H, H, bias=False)
         self.input_layernorm = RMSNorm(H, eps=config.rms_norm_eps)
@@ -57,7 +61,8 @@ class Eagle3DraftModel(nn.Module):
         self.post_attention_layernorm = RMSNorm(H, eps=config.rms_norm_eps)
         self.mlp = Qwen3MLP(H, config.intermediate_size, config.hidden_act)
         self.norm = RMSNorm(H, eps=config.rms_norm_eps)
-        self.lm_head = nn.Linear(H, config.vocab_size, bias=False)
+        self.lm_head = nn.Linear(H, draft_vocab, bias=False)
+        self.register_buffer("d2t", torch.zeros(draft_vocab, dtype=torch.int64), persistent=False)
         self.embed_tokens = None  # the target's embedding, bound by bind_target
 
     def bind_target(self, target):
@@ -81,7 +86,12 @@ class Eagle3DraftModel(nn.Module):
         return normed, out_feature
 
     def compute_logits(self, hidden_states):
+        """Logits over the draft vocabulary."""
         return self.lm_head(hidden_states)
+
+    def to_target(self, draft_ids):
+        """Draft-vocabulary ids -> target-vocabulary ids."""
+        return draft_ids + self.d2t[draft_ids]
 
     def attention_layers(self):
         return [self.self_attn.attn]

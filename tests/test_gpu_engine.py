@@ -154,6 +154,36 @@ def test_eagle3_graph_verify_greedy_is_target_argmax(dev):
     print("accepted-length histogram", dict(sorted(hist.items())), flush=True)
 
 
+@pytest.mark.gpu
+def test_eagle3_draft_vocabulary_maps_to_target_ids(dev):
+    """A draft head over a 64-token draft vocabulary whose d2t table scatters the draft
+    ids over a 512-token target vocabulary: the tree tokens are target ids from the
+    mapped set, and greedy output is still the target's argmax."""
+    llm = LLM("unused", hf_config=tiny_config(vocab=512, layers=6), num_kvcache_blocks=64,
+              speculative_method="eagle3", num_speculative_tokens=15, eagle_topk=4, eagle_depth=4,
+              eagle_draft_vocab=64, max_num_batched_tokens=4096)
+    runner = llm.model_runner
+    assert runner.draft.lm_head.weight.shape[0] == 64
+    ids = torch.arange(64, device=runner.draft.d2t.device)
+    runner.draft.d2t.copy_((ids * 7 + 3) % 512 - ids)
+    mapped = set(((ids * 7 + 3) % 512).tolist())
+    seen = set()
+    orig = runner._eagle_tree
+
+    def spy(*a):
+        toks, parents = orig(*a)
+        seen.update(toks.flatten().tolist())
+        return toks, parents
+
+    runner._eagle_tree = spy
+    rng = np.random.default_rng(6)
+    ps = [rng.integers(0, 512, size=n).tolist() for n in (40, 300)]
+    outs = llm.generate(ps, SamplingParams(temperature=0.0, max_tokens=24, ignore_eos=True),
+                        use_tqdm=False)
+    check_greedy_is_argmax(llm, ps, outs, 24)
+    assert seen and seen <= mapped
+
+
 def greedy_continuation(llm, ids, n):
     ids = list(ids)
     out = []
