@@ -1,7 +1,9 @@
 /*
  * nvx_spec.h -- C ABI of libnvx_spec.so, the MI355X (gfx950) speculative-decoding
  * verify path: n-gram drafter, paged tree attention, temperature softmax + tree /
- * chain rejection sampling, KV-cache slot scatter and accepted-path compaction.
+ * chain rejection sampling, KV-cache slot scatter and accepted-path compaction;
+ * beside them, the fused model layers the verify step runs around the attention
+ * and the EAGLE-3 draft head's top-k of log-probabilities.
  *
  * Conventions
  *   - Plain pointers to device memory, sizes in elements unless a name says
