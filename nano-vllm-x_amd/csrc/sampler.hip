@@ -1,8 +1,10 @@
 // Sampler kernels: temperature softmax and tree / chain rejection sampling.
 //
-// temperature_softmax: one workgroup per row, two streaming passes (online max and
-//   sum, then the fp32 write); 128-bit accesses when rows are 16-byte aligned.  HBM
-//   bound: logits read (the second pass mostly from the Infinity Cache) and fp32
+// temperature_softmax: one workgroup per row.  bf16 rows of the Qwen and Llama-3
+//   vocabulary sizes are read once into registers (max, sum and write from there);
+//   other rows take two streaming passes (online max and sum, then the fp32 write).
+//   128-bit accesses when rows are 16-byte aligned.  HBM bound: logits read (a
+//   streaming kernel's second pass mostly from the Infinity Cache) and fp32
 //   probabilities written once.
 //
 // rejection_sample_tree: one workgroup (1024 threads) per sequence walks the draft
@@ -140,6 +142,106 @@ __global__ __launch_bounds__(kVecNT) void softmax_vec_kernel(const VT* __restric
           __builtin_amdgcn_exp2f(__builtin_fmaf(x[e + 3], a, -M)) * inv);
   }
 }
+
+// ------------------------------------------------- softmax (row in registers)
+// bf16 rows of (NG-1)*8*kRegNT < V <= NG*8*kRegNT logits: each of the 512 threads
+// issues its NG 16-byte loads at once, so the row is read from HBM once and held
+// packed in registers (4 bytes per two logits); max, sum and the fp32 write then
+// work from registers.  Group u of thread t holds logits 8*(u*kRegNT + t) .. +7;
+// only the last group reaches past the row (its lanes past the row hold -inf and
+// store nothing).  One workgroup per CU (NG*4 + ~15 VGPRs), which alternates load,
+// reduce and store; the same math as the streaming kernel with the exact row max
+// instead of the online one.  Loads are raw buffer loads (one per-thread offset plus
+// a scalar offset per group); stores are global stores from a uniform row base.
+constexpr int kRegNT = 512;
+
+template <int NG>
+__global__ __launch_bounds__(kRegNT) void softmax_row_kernel(const uint16_t* __restrict__ logits,
+                                                             int64_t stride,
+                                                             const float* __restrict__ temps,
+                                                             float* __restrict__ probs, int V) {
+  using Tr = nvx::VecTraits<uint16_t>;
+  __shared__ float red[kRegNT / nvx::kWave];
+  const int row = blockIdx.x;
+  const float T = temps[row];
+  const int tid = threadIdx.x;
+  const int nvec = V / 8;
+  if (T == 0.f) {  // greedy row: fp32 logits unchanged
+    const uint4* src = reinterpret_cast<const uint4*>(logits + (int64_t)row * stride);
+    float* dst = probs + (int64_t)row * V;
+    for (int i = tid; i < nvec; i += kRegNT) {
+      float x[8];
+      Tr::expand(src[i], x);
+      *reinterpret_cast<float4*>(dst + (int64_t)i * 8) = make_float4(x[0], x[1], x[2], x[3]);
+      *reinterpret_cast<float4*>(dst + (int64_t)i * 8 + 4) = make_float4(x[4], x[5], x[6], x[7]);
+    }
+    return;
+  }
+  constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor word 3 (raw dword access)
+  const __amdgpu_buffer_rsrc_t in_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(logits + (int64_t)row * stride), 0, V * 2, kRsrcWord3);
+  const int voff = tid * 16;
+  const bool tail_ok = tid + (NG - 1) * kRegNT < nvec;
+  uint4 w[NG];
+#pragma unroll
+  for (int u = 0; u < NG - 1; ++u)
+    w[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(in_rsrc, voff, u * kRegNT * 16, 0));
+  w[NG - 1] = make_uint4(0xFF80FF80u, 0xFF80FF80u, 0xFF80FF80u, 0xFF80FF80u);  // bf16 -inf
+  if (tail_ok)
+    w[NG - 1] = __builtin_bit_cast(
+        uint4, __builtin_amdgcn_raw_buffer_load_b128(in_rsrc, voff, (NG - 1) * kRegNT * 16, 0));
+  float* const out_row = probs + (int64_t)row * V;
+  auto store = [&](int u, const float (&y)[8]) {
+    if (u < NG - 1 || tail_ok) {
+      float* d = out_row + (uint32_t)(tid * 8 + u * kRegNT * 8);
+      *reinterpret_cast<float4*>(d) = make_float4(y[0], y[1], y[2], y[3]);
+      *reinterpret_cast<float4*>(d + 4) = make_float4(y[4], y[5], y[6], y[7]);
+    }
+  };
+  // Each pass re-expands from the packed registers: without this the compiler keeps
+  // the expanded fp32 values of the first pass live (8 bytes per two logits).
+  auto opaque = [&]() {
+#pragma unroll
+    for (int u = 0; u < NG; ++u)
+      asm volatile("" : "+v"(w[u].x), "+v"(w[u].y), "+v"(w[u].z), "+v"(w[u].w));
+  };
+  const float a = 1.4426950408889634f / T;
+  float lm = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < NG; ++u) {
+    float x[8];
+    Tr::expand(w[u], x);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) lm = fmaxf(lm, x[e]);
+  }
+  const float M = nvx::block_max<kRegNT>(lm * a, red);
+  opaque();
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+  for (int u = 0; u < NG; ++u) {
+    float x[8];
+    Tr::expand(w[u], x);
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      s0 += __builtin_amdgcn_exp2f(__builtin_fmaf(x[e], a, -M));
+      s1 += __builtin_amdgcn_exp2f(__builtin_fmaf(x[e + 1], a, -M));
+    }
+  }
+  const float inv = 1.f / nvx::block_sum_any<kRegNT>(s0 + s1, red);
+  opaque();
+#pragma unroll
+  for (int u = 0; u < NG; ++u) {
+    float x[8];
+    Tr::expand(w[u], x);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[e], a, -M)) * inv;
+    store(u, x);
+  }
+}
+
+// Register-resident instantiations: 38 groups cover 151,553..155,648 logits (Qwen's
+// 151,936), 32 cover 126,977..131,072 (Llama-3's 128,256).
+inline int row_kernel_groups(int vocab) { return (vocab / 8 + kRegNT - 1) / kRegNT; }
 
 // --------------------------------------------------------- softmax (stream)
 __global__ __launch_bounds__(kNT) void softmax_stream_kernel(const void* __restrict__ logits,
@@ -487,7 +589,12 @@ extern "C" int nvx_temperature_softmax(const void* logits, int32_t logits_dtype,
   const int per = logits_dtype == NVX_DTYPE_BF16 ? 8 : 4;
   const bool vec = vocab % per == 0 && logits_row_stride % per == 0 && aligned16(logits) &&
                    aligned16(probs);
-  if (vec && logits_dtype == NVX_DTYPE_BF16) {
+  const int groups = row_kernel_groups(vocab);
+  if (vec && logits_dtype == NVX_DTYPE_BF16 && (groups == 38 || groups == 32)) {
+    hipLaunchKernelGGL(groups == 38 ? softmax_row_kernel<38> : softmax_row_kernel<32>,
+                       dim3(num_rows), dim3(kRegNT), 0, s, (const uint16_t*)logits,
+                       logits_row_stride, temperatures, probs, vocab);
+  } else if (vec && logits_dtype == NVX_DTYPE_BF16) {
     hipLaunchKernelGGL(softmax_vec_kernel<uint16_t>, dim3(num_rows), dim3(kVecNT), 0, s,
                        (const uint16_t*)logits, logits_row_stride, temperatures, probs, vocab);
   } else if (vec) {

@@ -35,6 +35,29 @@ def test_temperature_softmax(dev, dtype, V):
     assert np.array_equal(p[greedy], logits.float().numpy()[greedy])
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("V", [151560, 155648, 126984, 128256, 131072, 131080, 151936 + 8 * 512 * 4])
+def test_softmax_vocab_boundaries(dev, V):
+    """bf16 rows at the edges of the register-resident kernel's size classes (38 and 32
+    groups of 4 KB per 512 threads; 131,080 and 168,320 take the streaming kernel),
+    with padded rows (stride > V), masked logits (-inf) and greedy rows."""
+    g = torch.Generator().manual_seed(V)
+    N = 6
+    full = (torch.randn(N, V + 64, generator=g) * 2).to(torch.bfloat16)
+    full[1, : V // 2] = float("-inf")          # first half masked
+    full[3, torch.rand(V + 64, generator=g) < 0.9] = float("-inf")
+    full[4, V - 1] = 40.0                      # the row max in the last group's last lane
+    logits = full[:, :V]
+    temps = torch.tensor([0.7, 1.0, 0.0, 1.3, 0.9, 0.0])
+    print(f"[softmax] bf16 V={V} stride={full.stride(0)}", flush=True)
+    dl = full.to(dev)[:, :V]
+    p = temperature_softmax(dl, temps.to(dev)).cpu().numpy()
+    ref = osamp.temperature_softmax(logits.float().numpy(), temps.numpy())
+    np.testing.assert_allclose(p, ref, rtol=1e-5, atol=1e-35)
+    greedy = temps.numpy() == 0
+    assert np.array_equal(p[greedy], logits.float().numpy()[greedy])
+
+
 def tree_case(dev, B, T, V, depth, seed, greedy_frac=0.0, delta=False, same_pq=False,
               ragged=False, chain=False):
     rng = np.random.default_rng(seed)
