@@ -18,6 +18,11 @@ U[100, 1024], max_tokens U[100, 1024], temperature 0.6, ignore_eos, one warmup
 generate, wall-clock timing): Qwen3-0.6B architecture with random-init weights,
 drafting with a random-init EAGLE-3 head (T = 32 tree nodes) or without
 speculation (`--spec none`); value = output tokens/s.
+
+`--workload kernels` times each kernel of the path at its own workload (chain
+sampler, n-gram drafter, tree attention at the Qwen3-0.6B shape, and the KV
+scatter, compaction, softmax, tree rejection walk and draft top-k at the verify-step
+shape) against the oracle on the host, one JSON line per workload.
 """
 import argparse
 import json
@@ -50,7 +55,7 @@ def parse():
                     help="sequences in the CPU-baseline sample (0 disables it)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device copy (HBM counter calibration)")
-    ap.add_argument("--workload", choices=("verify", "e2e"), default="verify")
+    ap.add_argument("--workload", choices=("verify", "e2e", "kernels"), default="verify")
     ap.add_argument("--spec", choices=("eagle3", "ngram", "none"), default="eagle3",
                     help="e2e: speculative method")
     ap.add_argument("--e2e-seqs", type=int, default=256)
@@ -286,6 +291,224 @@ def cpu_baseline(args, torch, state, nseq):
     return float((acc + 1).sum()) / dt, cores, dt
 
 
+def run_kernels(args):
+    """Each kernel of the path at its own workload: the chain sampler (batch 8, k = 4),
+    the n-gram drafter (64 histories of 1024-4096 tokens, plus a scaled run), tree
+    attention at the Qwen3-0.6B shape (batch 32, 32-node trees), and the KV scatter,
+    compaction (worst case), softmax, tree rejection walk and draft top-k at the
+    Qwen3-8B verify-step shape.  GPU time per launch comes from the library's HIP-event
+    timers; the oracle runs on the host over the same inputs (or a stated sample, scaled
+    to the whole input) and checks the GPU result.  Prints one JSON line per workload."""
+    import numpy as np
+    import torch
+    from nanovllm import _C
+    from nanovllm.layers.attention import store_kvcache, tree_attention
+    from nanovllm.layers.sampler import (rejection_sample_chain, rejection_sample_tree,
+                                         temperature_softmax, topk_logprobs)
+    from nanovllm.spec.kv_compact import kv_compact
+    from nanovllm.spec.ngram import ngram_propose
+    from nanovllm.spec.tree import random_tree
+    from nanovllm.utils.synthetic import VerifyBatch, ngram_histories, pack_histories
+    from oracle import attention as oatt, draft as odraft, kvcache as okv, ngram as ong
+    from oracle import sampler as osamp
+
+    _C.lib()
+    dev = torch.device("cuda:0")
+    cores = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(cores)
+    V = 151936
+
+    def gpu_us(fn, timer, iters=20, warm=3):
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize()
+        _C.timing_reset()
+        _C.timing_enable(True)
+        for _ in range(iters):
+            fn()
+        torch.cuda.synchronize()
+        _C.timing_enable(False)
+        ms, n = _C.timing_read(timer)
+        return ms / n * 1e3
+
+    def cpu_us(fn, reps=1):
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            out = fn()
+        return (time.perf_counter() - t0) / reps * 1e6, out
+
+    def emit(kernel, workload, us, nbytes, cpu, sample, parity, note=None):
+        rec = {"workload": "kernels", "kernel": kernel, "config": workload, "gpu_us": us,
+               "algorithmic_bytes": nbytes,
+               "GBs": nbytes / (us * 1e-6) / 1e9 if nbytes else None,
+               "frac_of_hbm_peak": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS if nbytes else None,
+               "cpu_oracle_us": cpu, "cpu_cores": cores, "cpu_sample": sample,
+               "parity_with_oracle": parity}
+        if note:
+            rec["note"] = note
+        print(json.dumps(rec), flush=True)
+
+    def log(msg):
+        print(f"[bench kernels] {msg}", file=sys.stderr, flush=True)
+
+    # -- chain rejection sampling, batch 8, k = 4 (stochastic and greedy)
+    log("chain sampler")
+    g = torch.Generator().manual_seed(args.seed)
+    B, k = 8, 4
+    P = torch.softmax(torch.randn(B, k + 1, V, generator=g) * 2.0, -1)
+    Q = torch.softmax(torch.randn(B, k, V, generator=g) * 2.0, -1)
+    drafts = torch.stack([torch.multinomial(Q[b], 1, generator=g)[:, 0] for b in range(B)]).int()
+    rng = np.random.default_rng(args.seed)
+    U = torch.from_numpy(rng.random((B, k)).astype(np.float32))
+    Uf = torch.from_numpy(rng.random(B).astype(np.float32))
+    Pd, Qd, Dd, Ud, Ufd = (t.to(dev) for t in (P, Q, drafts, U, Uf))
+    for greedy in (False, True):
+        gmask = torch.full((B,), greedy, dtype=torch.bool)
+        gd = gmask.to(dev)
+        us = gpu_us(lambda: rejection_sample_chain(Pd, Qd, Dd, Ud, Ufd, gd), _C.TIMER_REJECTION)
+        acc, rec, bon, toks = (t.cpu().numpy() for t in rejection_sample_chain(Pd, Qd, Dd, Ud, Ufd, gd))
+        cus, ref = cpu_us(lambda: osamp.rejection_sample_chain(P.numpy(), Q.numpy(), drafts.numpy(),
+                                                               U.numpy(), Uf.numpy(), gmask.numpy()))
+        ok = all(np.array_equal(a, np.asarray(r)) for a, r in zip((acc, rec, bon, toks), ref))
+        emit("rejection_sample_chain", f"batch 8, k = 4, vocab {V}, fp32, "
+             f"{'greedy' if greedy else 'stochastic'}", us, float(B * (2 * k + 1) * V * 4), cus,
+             "the whole input", ok, "bytes are all P and Q rows; the walk reads only the rows it "
+             "visits")
+
+    # -- n-gram drafter: 64 histories of 1024-4096 tokens, and a scaled run
+    for name, nseq, lo, hi, sample in (("batch 64, lengths 1024-4096", 64, 1024, 4096, 64),
+                                       ("scaled: batch 256, lengths 16384-65536", 256, 16384, 65536, 16)):
+        log(f"n-gram drafter ({name})")
+        hist = ngram_histories(nseq, lo, hi, V, np.random.default_rng(args.seed + 1))
+        flat, offs = pack_histories(hist)
+        td, od = torch.from_numpy(flat).to(dev), torch.from_numpy(offs).to(dev)
+        us = gpu_us(lambda: ngram_propose(td, od, 3, 1, 5), _C.TIMER_NGRAM)
+        draft, dlen = (t.cpu().numpy() for t in ngram_propose(td, od, 3, 1, 5))
+        sflat, soffs = pack_histories(hist[:sample])
+        cus, (rdraft, rlen) = cpu_us(lambda: ong.ngram_propose(sflat, soffs, 3, 1, 5))
+        ok = np.array_equal(draft[:sample], rdraft) and np.array_equal(dlen[:sample], rlen)
+        emit("ngram_propose", f"{name}, k = 5, n = 3..1", us, float(4 * len(flat) + 8 * nseq * 5),
+             cus * nseq / sample, f"{sample} of {nseq} histories, scaled to {nseq}", ok)
+
+    # -- tree attention, Qwen3-0.6B shape: batch 32, ctx 1024-4096, 32-node depth-6 trees
+    log("tree attention (0.6B shape)")
+    B, T, Hq, Hkv, D = 32, 32, 16, 8, 128
+    rng = np.random.default_rng(args.seed + 2)
+    vb = VerifyBatch.random(B, (1024, 4096), T, 6, 256, rng)
+    g = torch.Generator().manual_seed(args.seed + 2)
+    kc = (torch.randn(vb.num_blocks, 256, Hkv, D, generator=g)).to(torch.bfloat16)
+    vc = (torch.randn(vb.num_blocks, 256, Hkv, D, generator=g)).to(torch.bfloat16)
+    N = int(vb.cu_q[-1])
+    q = torch.randn(N, Hq, D, generator=g).to(torch.bfloat16)
+    t = lambda a, dt=torch.int32: torch.from_numpy(a).to(dev, dt)
+    qd, kcd, vcd = q.to(dev), kc.to(dev), vc.to(dev)
+    a_args = (qd, kcd, vcd, t(vb.bt), t(vb.cu_q), t(vb.context_lens), D ** -0.5,
+              t(vb.masks, torch.int64), T, int(vb.context_lens.max()))
+    us = gpu_us(lambda: tree_attention(*a_args), _C.TIMER_TREE_ATTENTION)
+    o = tree_attention(*a_args).float().cpu().numpy()
+    ns = 4
+    rows = int(vb.cu_q[ns])
+    cus, ref = cpu_us(lambda: oatt.paged_attention(
+        q[:rows].float().numpy(), kc.float().numpy(), vc.float().numpy(), vb.bt[:ns],
+        vb.cu_q[:ns + 1], vb.context_lens[:ns], vb.masks[:rows].view(np.uint64), D ** -0.5, 256))
+    err = float(np.abs(o[:rows] - ref).max())
+    nbytes = float(vb.context_lens.sum()) * Hkv * D * 2 * 2 + 2.0 * N * Hq * D * 2
+    emit("tree_attention", "Qwen3-0.6B shape (16/8 heads, d 128), batch 32, ctx 1024-4096, "
+         "32-node depth-6 trees", us, nbytes, cus * B / ns, f"{ns} of {B} sequences, scaled",
+         err <= 2e-2, f"max abs error vs oracle on the sample {err:.2e} (tolerance 2e-2)")
+
+    # -- Qwen3-8B verify-step pieces: batch 64, 64-node trees, ctx 2048
+    B, T, Hkv, D, L = 64, 64, 8, 128, 36
+    rng = np.random.default_rng(args.seed + 3)
+    vb = VerifyBatch([2048] * B, [random_tree(T, 8, rng) for _ in range(B)], 256, rng)
+    N = B * T
+    log("store_kvcache")
+    g = torch.Generator().manual_seed(args.seed + 3)
+    kk = torch.randn(N, Hkv, D, generator=g).to(torch.bfloat16)
+    vv = torch.randn(N, Hkv, D, generator=g).to(torch.bfloat16)
+    kcd = torch.zeros(vb.num_blocks, 256, Hkv, D, dtype=torch.bfloat16, device=dev)
+    vcd = torch.zeros_like(kcd)
+    slots = t(vb.slot_mapping)
+    kkd, vvd = kk.to(dev), vv.to(dev)
+    us = gpu_us(lambda: store_kvcache(kkd, vvd, kcd, vcd, slots), _C.TIMER_STORE_KV)
+    kc_np = np.zeros((vb.num_blocks, 256, Hkv, D), np.uint16)
+    vc_np = np.zeros_like(kc_np)
+    kk_np, vv_np = kk.view(torch.int16).numpy().view(np.uint16), vv.view(torch.int16).numpy().view(np.uint16)
+    cus, _ = cpu_us(lambda: okv.store_kvcache(kk_np, vv_np, kc_np, vc_np, vb.slot_mapping))
+    ok = (np.array_equal(kcd.view(torch.int16).cpu().numpy().view(np.uint16), kc_np)
+          and np.array_equal(vcd.view(torch.int16).cpu().numpy().view(np.uint16), vc_np))
+    emit("store_kvcache", "4096 tree rows (64 x 64), 8 KV heads, d 128, bf16", us,
+         float(N * Hkv * D * 2 * 2 * 2), cus, "the whole input", ok)
+    del kcd, vcd
+
+    log("kv_compact (worst case)")
+    kc36 = torch.empty(L, vb.num_blocks, 256, Hkv, D, dtype=torch.bfloat16, device=dev)
+    vc36 = torch.empty_like(kc36)
+    path = torch.zeros(B, 9, dtype=torch.int32)
+    path[:, 1:] = torch.arange(1, 9, dtype=torch.int32) * 7  # 8 accepted nodes, path[d] >= d
+    acc = torch.full((B,), 8, dtype=torch.int32)
+    bt, ctx = t(vb.bt), t(vb.ctx)
+    pd, ad = path.to(dev), acc.to(dev)
+    us = gpu_us(lambda: kv_compact(kc36, vc36, bt, ctx, pd, ad), _C.TIMER_KV_COMPACT, iters=10)
+    # oracle on 2 of the 36 layers (bit patterns copied from the GPU caches)
+    k2 = kc36[:2].view(torch.int16).cpu().numpy().view(np.uint16).copy()
+    v2 = vc36[:2].view(torch.int16).cpu().numpy().view(np.uint16).copy()
+    kv_compact(kc36, vc36, bt, ctx, pd, ad)
+    cus, _ = cpu_us(lambda: okv.kv_compact(k2, v2, vb.bt, vb.ctx, path.numpy(), acc.numpy(), 256))
+    ok = (np.array_equal(kc36[:2].view(torch.int16).cpu().numpy().view(np.uint16), k2)
+          and np.array_equal(vc36[:2].view(torch.int16).cpu().numpy().view(np.uint16), v2))
+    emit("kv_compact", "36 layers, 64 sequences x 8 accepted rows (worst case), 8 KV heads, d 128",
+         us, float(B * 8 * L * 4 * Hkv * D * 2), cus * L / 2, "2 of 36 layers, scaled", ok)
+    del kc36, vc36
+
+    log("softmax, rejection walk, top-k")
+    g = torch.Generator(device=dev).manual_seed(args.seed + 4)
+    logits = (torch.randn(N, V, device=dev, generator=g) * 2).to(torch.bfloat16)
+    temps = torch.full((N,), 0.8, device=dev)
+    us = gpu_us(lambda: temperature_softmax(logits, temps), _C.TIMER_SOFTMAX)
+    probs = temperature_softmax(logits, temps)
+    ns = 64
+    lg = logits[:ns].float().cpu().numpy()
+    cus, ref = cpu_us(lambda: osamp.temperature_softmax(lg, np.full(ns, 0.8, np.float32)))
+    ok = bool(np.allclose(probs[:ns].cpu().numpy(), ref, rtol=1e-5, atol=1e-35))
+    emit("temperature_softmax", f"[4096, {V}] bf16 -> fp32, T = 0.8", us, float(N * V * 6),
+         cus * N / ns, f"{ns} of {N} rows, scaled", ok)
+
+    Pt = probs.view(B, T, V)
+    Qt = torch.softmax(torch.randn(B, T, V, device=dev, generator=g) * 2 / 0.8, -1)
+    parents = torch.from_numpy(np.stack(vb.parents)).to(dev)
+    toks = torch.zeros(B, T, dtype=torch.int32, device=dev)
+    child = torch.arange(1, T, device=dev)
+    for b in range(B):
+        drawn = torch.multinomial(Qt[b], T, replacement=True, generator=g)
+        toks[b, 1:] = drawn[parents[b, 1:].long(), child].int()
+    Ut = torch.rand(B, T, device=dev, generator=g)
+    Uft = torch.rand(B, device=dev, generator=g)
+    us = gpu_us(lambda: rejection_sample_tree(Pt, Qt, toks, parents, Ut, Uft), _C.TIMER_REJECTION)
+    pth, acc, otok, nxt = (x.cpu().numpy() for x in rejection_sample_tree(Pt, Qt, toks, parents, Ut, Uft))
+    ns = 4
+    Pn, Qn = Pt[:ns].cpu().numpy(), Qt[:ns].cpu().numpy()
+    cus, ref = cpu_us(lambda: osamp.rejection_sample_tree(
+        Pn, Qn, toks[:ns].cpu().numpy(), parents[:ns].cpu().numpy(), Ut[:ns].cpu().numpy(),
+        Uft[:ns].cpu().numpy(), np.zeros(ns, bool)))
+    ok = all(np.array_equal(a[:ns], np.asarray(r)) for a, r in zip((pth, acc, otok, nxt), ref))
+    emit("rejection_sample_tree", f"batch 64, 64-node depth-8 trees, vocab {V}, fp32, stochastic",
+         us, float(2 * B * T * V * 4), cus * B / ns, f"{ns} of {B} sequences, scaled", ok,
+         f"bytes are all P and Q rows; the walk reads only the rows it visits (mean accepted "
+         f"{float(acc.mean()):.2f})")
+
+    rows = 2048
+    us = gpu_us(lambda: topk_logprobs(logits[:rows], 8), _C.TIMER_TOPK)
+    lp, tk = topk_logprobs(logits[:rows], 8)
+    ns = 16
+    lg = logits[:ns].float().cpu().numpy()
+    cus, (rtok, rlp) = cpu_us(lambda: odraft.topk_logprobs(lg, 8))
+    ok = (np.array_equal(tk[:ns].cpu().numpy(), rtok)
+          and bool(np.all(np.abs(lp[:ns].cpu().numpy() - rlp) <= 2e-5 + 1e-6 * np.abs(rlp))))
+    emit("topk_logprobs", f"[{rows}, {V}] bf16, k = 8", us, float(rows * V * 2), cus * rows / ns,
+         f"{ns} of {rows} rows, scaled", ok)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -294,6 +517,9 @@ def main():
         sys.exit(2)
     if args.workload == "e2e":
         run_e2e(args)
+        return
+    if args.workload == "kernels":
+        run_kernels(args)
         return
     import torch
     from nanovllm import _C

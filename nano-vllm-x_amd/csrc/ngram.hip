@@ -12,7 +12,8 @@
 
 namespace {
 
-constexpr int kNT = 256;
+constexpr int kNT = 1024;
+constexpr int kUnroll = 4;
 constexpr int kMaxNgram = 8;
 
 __global__ __launch_bounds__(kNT) void ngram_kernel(const int32_t* __restrict__ tokens,
@@ -44,16 +45,30 @@ __global__ __launch_bounds__(kNT) void ngram_kernel(const int32_t* __restrict__ 
   for (int n = 0; n <= kMaxNgram; ++n) best[n] = INT32_MAX;
   int local_max = 0;
 
-  for (int e = 1 + threadIdx.x; e <= L - 1; e += kNT) {
-    int ml = 0;
+  // kUnroll window ends per thread per pass (e0, e0 + kNT, ...): their first
+  // comparison tokens are loaded together, so kUnroll coalesced loads per thread are
+  // in flight.  The deeper comparisons (t >= 1) only follow a first-token match.
+  for (int e0 = 1 + threadIdx.x; e0 <= L - 1; e0 += kNT * kUnroll) {
+    int32_t first[kUnroll];
 #pragma unroll
-    for (int t = 0; t < kMaxNgram; ++t) {
-      if (t < nmax && ml == t && e - 1 - t >= 0 && h[e - 1 - t] == suf[t]) ml = t + 1;
+    for (int u = 0; u < kUnroll; ++u) {
+      const int e = e0 + u * kNT;
+      first[u] = e <= L - 1 ? h[e - 1] : 0;
     }
-    local_max = max(local_max, ml);
 #pragma unroll
-    for (int n = 1; n <= kMaxNgram; ++n)
-      if (ml >= n && e < best[n]) best[n] = e;
+    for (int u = 0; u < kUnroll; ++u) {
+      const int e = e0 + u * kNT;
+      if (e > L - 1 || first[u] != suf[0]) continue;
+      int ml = 1;
+#pragma unroll
+      for (int t = 1; t < kMaxNgram; ++t) {
+        if (t < nmax && ml == t && e - 1 - t >= 0 && h[e - 1 - t] == suf[t]) ml = t + 1;
+      }
+      local_max = max(local_max, ml);
+#pragma unroll
+      for (int n = 1; n <= kMaxNgram; ++n)
+        if (ml >= n && e < best[n]) best[n] = e;
+    }
   }
 
   const int nstar = nvx::block_max_i<kNT>(local_max, red);
