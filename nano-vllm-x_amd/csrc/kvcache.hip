@@ -11,6 +11,7 @@ constexpr int kNT = 256;
 constexpr int kDepthGroup = 8;  // rows gathered into registers before scattering
 
 using vec16 = uint4;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------- scatter
 __global__ __launch_bounds__(kNT) void store_kv_vec_kernel(
@@ -49,11 +50,14 @@ __global__ __launch_bounds__(kNT) void store_kv_byte_kernel(
 }
 
 // ------------------------------------------------------------- compaction
-// One work item = (sequence, layer, K or V, 16-byte column of the row).  A
-// thread gathers up to kDepthGroup rows of its column into registers, then
-// scatters them.  Groups run in ascending depth; destinations ctx+d are always
-// below every later source ctx+path[d'] (path is strictly increasing), and
-// columns are disjoint across threads, so no ordering between threads is needed.
+// One workgroup per (sequence, layer).  The accepted rows' source and destination
+// slots depend only on the sequence, so the workgroup computes them once from
+// wave-uniform (scalar) loads of the path and block table.  Each thread then owns a
+// 16-byte column of the K or V row: it gathers up to kDepthGroup rows of its column
+// into registers, then scatters them.  Groups run in ascending depth; destinations
+// ctx+d are always below every later source ctx+path[d'] (path is strictly
+// increasing), and columns are disjoint across threads, so no ordering between
+// threads is needed.
 // Returns -1 for a position outside the block table or an unassigned (-1) entry so a
 // malformed path skips the row instead of touching memory outside the cache.
 __device__ __forceinline__ int64_t slot_of(const int32_t* bt, int bt_len, int pos, int bs) {
@@ -66,42 +70,38 @@ __global__ __launch_bounds__(kNT) void kv_compact_kernel(
     char* __restrict__ k_cache, char* __restrict__ v_cache, int64_t layer_stride, int num_layers,
     int vecs_per_row, int block_size, const int32_t* __restrict__ block_tables, int bt_stride,
     const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ path, int path_stride,
-    const int32_t* __restrict__ accepted_len, int num_seqs) {
-  const int64_t per_seq = (int64_t)num_layers * 2 * vecs_per_row;
-  const int64_t total = per_seq * num_seqs;
+    const int32_t* __restrict__ accepted_len) {
+  const int b = blockIdx.x / num_layers;
+  const int layer = blockIdx.x - b * num_layers;
+  const int a = min(accepted_len[b], path_stride - 1);
+  if (a <= 0) return;  // uniform over the workgroup
+  const int32_t* bt = block_tables + (int64_t)b * bt_stride;
+  const int32_t* pth = path + (int64_t)b * path_stride;
+  const int ctx = ctx_lens[b];
   const int64_t row_bytes = (int64_t)vecs_per_row * 16;
-  for (int64_t i = (int64_t)blockIdx.x * kNT + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * kNT) {
-    const int b = (int)(i / per_seq);
-    int64_t r = i - (int64_t)b * per_seq;
-    const int a = min(accepted_len[b], path_stride - 1);
-    if (a <= 0) continue;
-    const int layer_kv = (int)(r / vecs_per_row);
-    const int v = (int)(r - (int64_t)layer_kv * vecs_per_row);
-    const int layer = layer_kv >> 1;
-    char* base = ((layer_kv & 1) ? v_cache : k_cache) + layer * layer_stride + v * 16;
-    const int32_t* bt = block_tables + (int64_t)b * bt_stride;
-    const int32_t* pth = path + (int64_t)b * path_stride;
-    const int ctx = ctx_lens[b];
-    for (int d0 = 1; d0 <= a; d0 += kDepthGroup) {
-      vec16 rows[kDepthGroup];
+  char* const kl = k_cache + layer * layer_stride;
+  char* const vl = v_cache + layer * layer_stride;
+  for (int d0 = 1; d0 <= a; d0 += kDepthGroup) {
+    int64_t src[kDepthGroup], dst[kDepthGroup];
 #pragma unroll
-      for (int j = 0; j < kDepthGroup; ++j) {
-        const int d = d0 + j;
-        if (d <= a) {
-          const int64_t src = slot_of(bt, bt_stride, ctx + pth[d], block_size);
-          if (src >= 0) rows[j] = *reinterpret_cast<const vec16*>(base + src * row_bytes);
-        }
-      }
+    for (int j = 0; j < kDepthGroup; ++j) {
+      const int d = d0 + j;
+      src[j] = d <= a ? slot_of(bt, bt_stride, ctx + pth[d], block_size) : -1;
+      dst[j] = d <= a ? slot_of(bt, bt_stride, ctx + d, block_size) : -1;
+    }
+    for (int col = threadIdx.x; col < 2 * vecs_per_row; col += kNT) {
+      char* const base = (col < vecs_per_row ? kl : vl) + (col % vecs_per_row) * 16;
+      // Unconditional loads (a row with no valid source reads slot 0 and is not
+      // stored) keep the gathered rows in registers with all loads in flight.  The
+      // rows are a native 4 x u32 vector type: an array of HIP's uint4 struct here
+      // was kept in scratch memory.
+      u32x4 rows[kDepthGroup];
 #pragma unroll
-      for (int j = 0; j < kDepthGroup; ++j) {
-        const int d = d0 + j;
-        if (d <= a) {
-          const int64_t src = slot_of(bt, bt_stride, ctx + pth[d], block_size);
-          const int64_t dst = slot_of(bt, bt_stride, ctx + d, block_size);
-          if (src >= 0 && dst >= 0) *reinterpret_cast<vec16*>(base + dst * row_bytes) = rows[j];
-        }
-      }
+      for (int j = 0; j < kDepthGroup; ++j)
+        rows[j] = *reinterpret_cast<const u32x4*>(base + max(src[j], (int64_t)0) * row_bytes);
+#pragma unroll
+      for (int j = 0; j < kDepthGroup; ++j)
+        if (src[j] >= 0 && dst[j] >= 0) *reinterpret_cast<u32x4*>(base + dst[j] * row_bytes) = rows[j];
     }
   }
 }
@@ -167,10 +167,11 @@ extern "C" int nvx_kv_compact(void* k_cache, void* v_cache, int64_t layer_stride
   hipStream_t s = (hipStream_t)stream;
   nvx::TimerScope timer(NVX_TIMER_KV_COMPACT, s);
   const int vpr = row_bytes / 16;
-  const int64_t work = (int64_t)num_seqs * num_layers * 2 * vpr;
-  hipLaunchKernelGGL(kv_compact_kernel, dim3(grid_for(work)), dim3(kNT), 0, s, (char*)k_cache,
+  const int64_t blocks = (int64_t)num_seqs * num_layers;
+  NVX_CHECK(blocks < (1ll << 31), "kv_compact: too many (sequence, layer) pairs");
+  hipLaunchKernelGGL(kv_compact_kernel, dim3((unsigned)blocks), dim3(kNT), 0, s, (char*)k_cache,
                      (char*)v_cache, layer_stride_bytes, num_layers, vpr, block_size, block_tables,
-                     block_table_stride, ctx_lens, path, path_stride, accepted_len, num_seqs);
+                     block_table_stride, ctx_lens, path, path_stride, accepted_len);
   NVX_LAUNCHED();
   return NVX_OK;
 }
