@@ -371,9 +371,9 @@ def run_kernels(args):
                                                                U.numpy(), Uf.numpy(), gmask.numpy()))
         ok = all(np.array_equal(a, np.asarray(r)) for a, r in zip((acc, rec, bon, toks), ref))
         emit("rejection_sample_chain", f"batch 8, k = 4, vocab {V}, fp32, "
-             f"{'greedy' if greedy else 'stochastic'}", us, float(B * (2 * k + 1) * V * 4), cus,
-             "the whole input", ok, "bytes are all P and Q rows; the walk reads only the rows it "
-             "visits")
+             f"{'greedy' if greedy else 'stochastic'}", us, None, cus, "the whole input", ok,
+             f"latency-bound walk: reads only the rows it visits, at most all P and Q rows "
+             f"({B * (2 * k + 1) * V * 4 / 1e6:.1f} MB)")
 
     # -- n-gram drafter: 64 histories of 1024-4096 tokens, and a scaled run
     for name, nseq, lo, hi, sample in (("batch 64, lengths 1024-4096", 64, 1024, 4096, 64),
@@ -493,9 +493,9 @@ def run_kernels(args):
         Uft[:ns].cpu().numpy(), np.zeros(ns, bool)))
     ok = all(np.array_equal(a[:ns], np.asarray(r)) for a, r in zip((pth, acc, otok, nxt), ref))
     emit("rejection_sample_tree", f"batch 64, 64-node depth-8 trees, vocab {V}, fp32, stochastic",
-         us, float(2 * B * T * V * 4), cus * B / ns, f"{ns} of {B} sequences, scaled", ok,
-         f"bytes are all P and Q rows; the walk reads only the rows it visits (mean accepted "
-         f"{float(acc.mean()):.2f})")
+         us, None, cus * B / ns, f"{ns} of {B} sequences, scaled", ok,
+         f"latency-bound walk: reads only the rows it visits, at most all P and Q rows "
+         f"({2 * B * T * V * 4 / 1e6:.0f} MB); mean accepted {float(acc.mean()):.2f}")
 
     rows = 2048
     us = gpu_us(lambda: topk_logprobs(logits[:rows], 8), _C.TIMER_TOPK)
