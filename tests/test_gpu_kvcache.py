@@ -45,10 +45,10 @@ def test_store_kvcache_asserts(dev):
         store_kvcache(k, k, cache, cache, torch.zeros(3, dtype=torch.int32, device=dev))
 
 
-def compact_case(dev, B, L, T, depth, seed, block_size=256):
+def compact_case(dev, B, L, T, depth, seed, block_size=256, Hkv=8, D=128):
     rng = np.random.default_rng(seed)
     g = torch.Generator().manual_seed(seed)
-    Hkv, D = 8, 128
+    print(f"[compact] B={B} L={L} T={T} depth={depth} Hkv={Hkv} D={D} seed={seed}", flush=True)
     ctx = rng.integers(1, 3000, size=B).astype(np.int32)
     bt, nblk = paged_block_tables(ctx + T, block_size, rng)
     kc = torch.randn(L, nblk, block_size, Hkv, D, generator=g).to(torch.bfloat16)
@@ -92,3 +92,17 @@ def test_kv_compact_small(dev):
 def test_kv_compact_config4_shape(dev):
     """64 sequences, 36 layers, 64-node depth-8 trees (Qwen3-8B verify step)."""
     compact_case(dev, B=64, L=36, T=64, depth=8, seed=2)
+
+
+@pytest.mark.gpu
+def test_kv_compact_deep_paths(dev):
+    """Accepted paths of up to 30 rows: several 8-row gather/scatter groups in sequence."""
+    compact_case(dev, B=6, L=2, T=40, depth=30, seed=3)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("Hkv,D", [(2, 64), (16, 256)])
+def test_kv_compact_row_widths(dev, Hkv, D):
+    """256-byte rows (fewer columns than threads) and 8 KiB rows (each thread moves
+    several columns)."""
+    compact_case(dev, B=5, L=2, T=24, depth=10, seed=4 + Hkv, Hkv=Hkv, D=D)

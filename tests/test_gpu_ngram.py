@@ -40,6 +40,17 @@ def test_edge_cases(dev, max_n, min_n, k):
 
 
 @pytest.mark.gpu
+def test_long_histories(dev):
+    """Histories of 10k-70k tokens (several 4096-window passes per thread block), and
+    small-vocabulary histories where most windows match the first suffix token."""
+    rng = np.random.default_rng(5)
+    hist = ngram_histories(6, 10000, 70000, 151936, rng)
+    hist += [rng.integers(0, v, size=n).astype(np.int32) for v, n in ((3, 20000), (20, 50000), (2, 9000))]
+    run(dev, hist)
+    run(dev, hist, 8, 2, 9)
+
+
+@pytest.mark.gpu
 def test_scaled_batch(dev):
     rng = np.random.default_rng(3)
     hist = ngram_histories(1024, 1024, 4096, 151936, rng)
