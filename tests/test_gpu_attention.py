@@ -145,3 +145,22 @@ def test_attention_module_store_then_attend(dev):
     ref = oatt.paged_attention(q.float().numpy(), kf, vf, vb.bt, vb.cu_q, vb.context_lens,
                                vb.masks.view(np.uint64), D ** -0.5, 256)
     assert np.abs(o.cpu().float().numpy() - ref).max() < TOL
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", range(8))
+def test_random_shapes(dev, case):
+    """Seeded sweep: GQA group sizes 1-16 (including 5, as 40 q / 8 KV heads), batches
+    of 1-6, cached contexts of 0-12k tokens (tree keys only, partial last chunks, many
+    KV splits), trees of 1-64 nodes; a few cases causal instead of tree-masked."""
+    rng = np.random.default_rng(1000 + case)
+    Hq, Hkv = [(40, 8), (64, 4), (8, 8), (32, 8), (20, 4), (16, 8), (48, 8), (16, 1)][case]
+    B = int(rng.integers(1, 7))
+    ctx = [int(rng.choice([0, rng.integers(1, 70), rng.integers(70, 3000), rng.integers(3000, 12000)]))
+           for _ in range(B)]
+    trees = [random_tree(int(t), int(min(t - 1, rng.integers(1, 10))), rng)
+             for t in rng.integers(1, 65, size=B)]
+    causal = case % 4 == 3
+    if causal:
+        trees = [chain_parents(len(t)) for t in trees]
+    run_case(dev, Hq, Hkv, ctx, trees, seed=2000 + case, causal=causal)
