@@ -1,7 +1,8 @@
 /*
  * nvx_spec.h -- C ABI of libnvx_spec.so, the MI355X (gfx950) speculative-decoding
  * verify path: n-gram drafter, paged tree attention, temperature softmax + tree /
- * chain rejection sampling, KV-cache slot scatter and accepted-path compaction;
+ * chain rejection sampling (also fused, without materialising the probabilities),
+ * KV-cache slot scatter and accepted-path compaction;
  * beside them, the fused model layers the verify step runs around the attention
  * and the EAGLE-3 draft head's top-k of log-probabilities.
  *
@@ -157,6 +158,44 @@ int nvx_rejection_sample_tree(const float* target_probs, int64_t p_seq_stride,
                               const uint8_t* greedy, int32_t draft_mode, int32_t num_seqs,
                               int32_t* path, int32_t* accepted_len, int32_t* out_tokens,
                               int32_t* next_token, void* stream);
+
+/* ------------------------------------ fused softmax + tree rejection sampling --
+ * Tree verification from the target logits without writing fp32 probabilities: one
+ * streaming pass reads every logits row for its statistics, then the walk reads only
+ * the rows it visits and recomputes each probability it needs.  No counterpart in
+ * the reference; it fuses the softmax of Sampler.forward (reference
+ * nanovllm/layers/sampler.py:9-10) into the walk.
+ *
+ * nvx_softmax_stats: per logits row r (temperature T = temperatures[r]), one online
+ *   pass gives stats[2r] = max_y(logit[y]) * log2(e)/T and stats[2r+1] = 1 / sum_y
+ *   exp2(logit[y] * log2(e)/T - stats[2r]) (fp32, within 1e-5 relative of the exact
+ *   values); T == 0 rows get (0, 0).  Logits rows must be 16-byte aligned with vocab
+ *   and row stride multiples of 8 (bf16) or 4 (fp32).
+ * nvx_softmax_from_stats: probs[r][y] = exp2(fma(logit[y], log2(e)/T, -stats[2r])) *
+ *   stats[2r+1], or logit[y] when T == 0: the probabilities the fused walk uses (same
+ *   alignment rules; probs 16-byte aligned, [num_rows, vocab] contiguous).
+ * nvx_rejection_sample_tree_logits: nvx_rejection_sample_tree with target row (b, i)
+ *   given as logits row b*node_stride + i (logits_row_stride elements apart), its
+ *   temperature and its stats.  Its outputs are bit for bit those of
+ *   nvx_rejection_sample_tree on the rows nvx_softmax_from_stats writes.  Other
+ *   arguments and outputs as nvx_rejection_sample_tree.
+ */
+int nvx_softmax_stats(const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
+                      const float* temperatures, float* stats, int32_t num_rows, int32_t vocab,
+                      void* stream);
+int nvx_softmax_from_stats(const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
+                           const float* temperatures, const float* stats, float* probs,
+                           int32_t num_rows, int32_t vocab, void* stream);
+int nvx_rejection_sample_tree_logits(const void* logits, int32_t logits_dtype,
+                                     int64_t logits_row_stride, const float* temperatures,
+                                     const float* stats, const float* draft_probs,
+                                     int64_t q_seq_stride, int32_t vocab, const int32_t* tokens,
+                                     const int32_t* parents, const int32_t* num_nodes,
+                                     int32_t node_stride, const float* uniforms,
+                                     const float* final_uniforms, const uint8_t* greedy,
+                                     int32_t draft_mode, int32_t num_seqs, int32_t* path,
+                                     int32_t* accepted_len, int32_t* out_tokens,
+                                     int32_t* next_token, void* stream);
 
 /* -------------------------------------------------- fused model layers --
  * Elementwise layers of the target model around the verify-path attention, each

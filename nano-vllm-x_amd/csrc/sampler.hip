@@ -35,20 +35,27 @@ __device__ __forceinline__ float load_logit(const void* row, int i, int dtype) {
 
 // ------------------------------------------------------- softmax (vectorised)
 // One 1024-thread workgroup per row, two streaming passes over the logits: online
-// max / sum in log2 units (x * log2(e) / T) with eight 16-byte loads in flight per
-// thread, then exp2(fma(x, log2(e)/T, -max)) * (1/sum) written as 128-bit stores.
+// max / sum in log2 units (x * log2(e) / T) with kU (eight for the softmax) 16-byte
+// loads in flight per thread, then exp2(fma(x, log2(e)/T, -max)) * (1/sum) written as
+// 128-bit stores.
 // With at most two rows per CU in flight (~150 MB of rows GPU-wide) the second
 // read of a row is served by the Infinity Cache.  1/T folded into the FMA
 // keeps the relative error ~1e-6 (contract tolerance 1e-5).
 constexpr int kVecNT = 1024;
-constexpr int kUnroll = 8;
 
-
-template <typename VT>
+// Modes of the streaming kernel.  kSoftmax: both passes.  kStatsOnly: the first pass
+// only; stores (max in log2 units, 1/sum) for the row in stats[row] (the fused
+// rejection walk recomputes each probability it reads).  kFromStats: the second pass
+// only, with the row's statistics read from stats[row] (probabilities bit for bit as
+// the fused walk computes them).  kU: 16-byte loads in flight per thread.
+enum { kSoftmax = 0, kStatsOnly = 1, kFromStats = 2 };
+template <typename VT, int kMode = kSoftmax, int kU = 8>
 __global__ __launch_bounds__(kVecNT) void softmax_vec_kernel(const VT* __restrict__ logits,
                                                              int64_t stride,
                                                              const float* __restrict__ temps,
-                                                             float* __restrict__ probs, int V) {
+                                                             float* __restrict__ probs, int V,
+                                                             float2* __restrict__ stats) {
+  constexpr int kUnroll = kU;
   using Tr = nvx::VecTraits<VT>;
   constexpr int P = Tr::kPer;
   __shared__ float red[kVecNT / nvx::kWave];
@@ -59,6 +66,10 @@ __global__ __launch_bounds__(kVecNT) void softmax_vec_kernel(const VT* __restric
   const int nvec = V / P;
   const int tid = threadIdx.x;
   if (T == 0.f) {  // greedy row: fp32 logits unchanged
+    if constexpr (kMode == kStatsOnly) {
+      if (tid == 0) stats[row] = make_float2(0.f, 0.f);
+      return;
+    }
     for (int i = tid; i < nvec; i += kVecNT) {
       float x[P];
       Tr::expand(src[i], x);
@@ -69,47 +80,57 @@ __global__ __launch_bounds__(kVecNT) void softmax_vec_kernel(const VT* __restric
     return;
   }
   const float a = 1.4426950408889634f / T;
-  float m = -INFINITY, s = 0.f;
+  float M, inv;
   int i = tid;
-  for (; i + (kUnroll - 1) * kVecNT < nvec; i += kUnroll * kVecNT) {
-    uint4 w[kUnroll];
+  if constexpr (kMode == kFromStats) {
+    M = stats[row].x;
+    inv = stats[row].y;
+  } else {
+    float m = -INFINITY, s = 0.f;
+    for (; i + (kUnroll - 1) * kVecNT < nvec; i += kUnroll * kVecNT) {
+      uint4 w[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) w[u] = src[i + u * kVecNT];
-    float lm = -INFINITY;
-    float x[kUnroll][P];
+      for (int u = 0; u < kUnroll; ++u) w[u] = src[i + u * kVecNT];
+      float lm = -INFINITY;
+      float x[kUnroll][P];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      Tr::expand(w[u], x[u]);
+      for (int u = 0; u < kUnroll; ++u) {
+        Tr::expand(w[u], x[u]);
 #pragma unroll
-      for (int e = 0; e < P; ++e) lm = fmaxf(lm, x[u][e]);
+        for (int e = 0; e < P; ++e) lm = fmaxf(lm, x[u][e]);
+      }
+      const float mn = fmaxf(m, lm * a);
+      if (mn == -INFINITY) continue;  // every value so far is -inf
+      float acc = 0.f;
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+        for (int e = 0; e < P; ++e) acc += __builtin_amdgcn_exp2f(__builtin_fmaf(x[u][e], a, -mn));
+      s = (m == -INFINITY ? 0.f : s * __builtin_amdgcn_exp2f(m - mn)) + acc;
+      m = mn;
     }
-    const float mn = fmaxf(m, lm * a);
-    if (mn == -INFINITY) continue;  // every value so far is -inf
-    float acc = 0.f;
+    for (; i < nvec; i += kVecNT) {
+      float x[P];
+      Tr::expand(src[i], x);
+      float lm = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u)
+      for (int e = 0; e < P; ++e) lm = fmaxf(lm, x[e]);
+      const float mn = fmaxf(m, lm * a);
+      if (mn == -INFINITY) continue;
+      float acc = 0.f;
 #pragma unroll
-      for (int e = 0; e < P; ++e) acc += __builtin_amdgcn_exp2f(__builtin_fmaf(x[u][e], a, -mn));
-    s = (m == -INFINITY ? 0.f : s * __builtin_amdgcn_exp2f(m - mn)) + acc;
-    m = mn;
+      for (int e = 0; e < P; ++e) acc += __builtin_amdgcn_exp2f(__builtin_fmaf(x[e], a, -mn));
+      s = (m == -INFINITY ? 0.f : s * __builtin_amdgcn_exp2f(m - mn)) + acc;
+      m = mn;
+    }
+    M = nvx::block_max<kVecNT>(m, red);
+    const float part = (m == -INFINITY) ? 0.f : s * __builtin_amdgcn_exp2f(m - M);
+    inv = 1.f / nvx::block_sum_any<kVecNT>(part, red);
+    if constexpr (kMode == kStatsOnly) {
+      if (tid == 0) stats[row] = make_float2(M, inv);
+      return;
+    }
   }
-  for (; i < nvec; i += kVecNT) {
-    float x[P];
-    Tr::expand(src[i], x);
-    float lm = -INFINITY;
-#pragma unroll
-    for (int e = 0; e < P; ++e) lm = fmaxf(lm, x[e]);
-    const float mn = fmaxf(m, lm * a);
-    if (mn == -INFINITY) continue;
-    float acc = 0.f;
-#pragma unroll
-    for (int e = 0; e < P; ++e) acc += __builtin_amdgcn_exp2f(__builtin_fmaf(x[e], a, -mn));
-    s = (m == -INFINITY ? 0.f : s * __builtin_amdgcn_exp2f(m - mn)) + acc;
-    m = mn;
-  }
-  const float M = nvx::block_max<kVecNT>(m, red);
-  const float part = (m == -INFINITY) ? 0.f : s * __builtin_amdgcn_exp2f(m - M);
-  const float inv = 1.f / nvx::block_sum_any<kVecNT>(part, red);
   i = tid;
   for (; i + (kUnroll - 1) * kVecNT < nvec; i += kUnroll * kVecNT) {
     uint4 w[kUnroll];
@@ -301,7 +322,7 @@ __device__ __forceinline__ float cur_eval(const Residual& r, float py, float qy,
   return fmaxf(py - r.c * qy, 0.f) / r.Z;
 }
 
-__device__ __forceinline__ void load4(const float* row, int g, int V, bool vec, float out[4]) {
+__device__ __forceinline__ void load4f(const float* row, int g, int V, bool vec, float out[4]) {
   const int i0 = 4 * g;
   if (vec && i0 + 3 < V) {
     const float4 t = reinterpret_cast<const float4*>(row)[g];
@@ -312,10 +333,82 @@ __device__ __forceinline__ void load4(const float* row, int g, int V, bool vec, 
   }
 }
 
+// Sources of the target distribution read by the walk.  ProbRow: fp32 probability
+// rows (the softmax output).  LogitRow: the row's logits with its statistics from
+// nvx_softmax_stats; each probability is recomputed as exp2(fma(x, log2(e)/T, -max)) *
+// (1/sum), or x itself at temperature 0, the values nvx_softmax_from_stats writes for
+// the same statistics.
+struct ProbRow {
+  const float* row;
+  __device__ __forceinline__ void load4(int g, int V, bool vec, float out[4]) const {
+    load4f(row, g, V, vec, out);
+  }
+  __device__ __forceinline__ float at(int y) const { return row[y]; }
+};
+
+template <typename VT>
+struct LogitRow {
+  const VT* row;
+  float a, M, inv;
+  bool raw;  // temperature 0: the softmax passes the fp32 logits through
+  __device__ __forceinline__ float prob(float x) const {
+    return raw ? x : __builtin_amdgcn_exp2f(__builtin_fmaf(x, a, -M)) * inv;
+  }
+  __device__ __forceinline__ static float val(const VT* r, int i) {
+    if constexpr (sizeof(VT) == 2) return nvx::bf16_lo((uint32_t)reinterpret_cast<const uint16_t*>(r)[i]);
+    else return reinterpret_cast<const float*>(r)[i];
+  }
+  __device__ __forceinline__ void load4(int g, int V, bool vec, float out[4]) const {
+    const int i0 = 4 * g;
+    float x[4];
+    if (vec && i0 + 3 < V) {
+      if constexpr (sizeof(VT) == 2) {
+        const uint2 w = reinterpret_cast<const uint2*>(row)[g];
+        x[0] = nvx::bf16_lo(w.x); x[1] = nvx::bf16_hi(w.x);
+        x[2] = nvx::bf16_lo(w.y); x[3] = nvx::bf16_hi(w.y);
+      } else {
+        const float4 t = reinterpret_cast<const float4*>(row)[g];
+        x[0] = t.x; x[1] = t.y; x[2] = t.z; x[3] = t.w;
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) x[c] = (i0 + c < V) ? val(row, i0 + c) : 0.f;
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) out[c] = (i0 + c < V) ? prob(x[c]) : 0.f;
+  }
+  __device__ __forceinline__ float at(int y) const { return prob(val(row, y)); }
+};
+
+struct ProbSource {
+  const float* P;
+  int64_t seq_stride;
+  int V;
+  __device__ __forceinline__ ProbRow row(int b, int cur) const {
+    return {P + (int64_t)b * seq_stride + (int64_t)cur * V};
+  }
+};
+
+template <typename VT>
+struct LogitSource {
+  const VT* L;
+  int64_t row_stride;  // elements between logits rows; sequence b's node i is row b*rows_per_seq + i
+  int rows_per_seq;
+  const float* temps;   // per logits row
+  const float2* stats;  // per logits row: (max in log2 units, 1/sum)
+  __device__ __forceinline__ LogitRow<VT> row(int b, int cur) const {
+    const int64_t r = (int64_t)b * rows_per_seq + cur;
+    const float T = temps[r];
+    const float2 st = stats[r];
+    return {L + r * row_stride, 1.4426950408889634f / T, st.x, st.y, T == 0.f};
+  }
+};
+
 // Canonical sum over y of max(p[y] - c*q[y], 0) (the un-normalised stochastic
 // residual for multiplier c).  Four groups per lane are loaded before they are
 // accumulated (in the same order) to keep more bytes in flight.
-__device__ float residual_sum(const float* prow, const float* qrow, int V, bool vec, float c,
+template <typename PRow>
+__device__ float residual_sum(const PRow& prow, const float* qrow, int V, bool vec, float c,
                               float* red) {
   const int G = (V + 3) / 4;
   float acc = 0.f;
@@ -324,8 +417,8 @@ __device__ float residual_sum(const float* prow, const float* qrow, int V, bool 
     float p[4][4], q[4][4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      load4(prow, g + u * kNT, V, vec, p[u]);
-      load4(qrow, g + u * kNT, V, vec, q[u]);
+      prow.load4(g + u * kNT, V, vec, p[u]);
+      load4f(qrow, g + u * kNT, V, vec, q[u]);
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u)
@@ -334,8 +427,8 @@ __device__ float residual_sum(const float* prow, const float* qrow, int V, bool 
   }
   for (; g < G; g += kNT) {
     float p[4], q[4];
-    load4(prow, g, V, vec, p);
-    load4(qrow, g, V, vec, q);
+    prow.load4(g, V, vec, p);
+    load4f(qrow, g, V, vec, q);
 #pragma unroll
     for (int e = 0; e < 4; ++e)
       if (4 * g + e < V) acc = acc + fmaxf(p[e] - c * q[e], 0.f);
@@ -345,7 +438,8 @@ __device__ float residual_sum(const float* prow, const float* qrow, int V, bool 
 
 // Inverse-CDF pick from the current distribution with uniform u (contract in
 // oracle/sampler.py: cdf_pick).
-__device__ int cdf_pick(const float* prow, const float* qrow, int V, bool vec, const Residual& r,
+template <typename PRow>
+__device__ int cdf_pick(const PRow& prow, const float* qrow, int V, bool vec, const Residual& r,
                         float u, float* red, int* redi, float* incl_lds) {
   const int C = 4 * (((V + 3) / 4 + kNT - 1) / kNT);
   const int lo = threadIdx.x * C;
@@ -357,8 +451,8 @@ __device__ int cdf_pick(const float* prow, const float* qrow, int V, bool vec, c
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       if (i + 4 * u < hi) {
-        load4(prow, i / 4 + u, V, vec, p[u]);
-        if (!r.delta) load4(qrow, i / 4 + u, V, vec, q[u]);
+        prow.load4(i / 4 + u, V, vec, p[u]);
+        if (!r.delta) load4f(qrow, i / 4 + u, V, vec, q[u]);
       }
     }
 #pragma unroll
@@ -379,8 +473,8 @@ __device__ int cdf_pick(const float* prow, const float* qrow, int V, bool vec, c
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       if (i + 4 * u < hi) {
-        load4(prow, i / 4 + u, V, vec, p[u]);
-        if (!r.delta) load4(qrow, i / 4 + u, V, vec, q[u]);
+        prow.load4(i / 4 + u, V, vec, p[u]);
+        if (!r.delta) load4f(qrow, i / 4 + u, V, vec, q[u]);
       }
     }
 #pragma unroll
@@ -406,7 +500,8 @@ __device__ int cdf_pick(const float* prow, const float* qrow, int V, bool vec, c
 }
 
 // First index of the row maximum.
-__device__ int block_argmax(const float* row, int V, bool vec, float* red, int* redi) {
+template <typename PRow>
+__device__ int block_argmax(const PRow& row, int V, bool vec, float* red, int* redi) {
   float bv = -INFINITY;
   int bi = INT32_MAX;
   const int G = (V + 3) / 4;
@@ -414,7 +509,7 @@ __device__ int block_argmax(const float* row, int V, bool vec, float* red, int* 
     float p[4][4];
 #pragma unroll
     for (int u = 0; u < 4; ++u)
-      if (g0 + u * kNT < G) load4(row, g0 + u * kNT, V, vec, p[u]);
+      if (g0 + u * kNT < G) row.load4(g0 + u * kNT, V, vec, p[u]);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int g = g0 + u * kNT;
@@ -460,8 +555,9 @@ __device__ int block_argmax(const float* row, int V, bool vec, float* red, int* 
   return r == INT32_MAX ? 0 : r;
 }
 
+template <typename Src>
 __global__ __launch_bounds__(kNT) void rejection_tree_kernel(
-    const float* __restrict__ P, int64_t p_seq_stride, const float* __restrict__ Q,
+    Src src, const float* __restrict__ Q,
     int64_t q_seq_stride, int V, const int32_t* __restrict__ tokens,
     const int32_t* __restrict__ parents, const int32_t* __restrict__ num_nodes, int node_stride,
     const float* __restrict__ U, const float* __restrict__ U_final,
@@ -490,7 +586,7 @@ __global__ __launch_bounds__(kNT) void rejection_tree_kernel(
   int cur = 0, depth = 0, next = 0;
   if (threadIdx.x == 0) s_path[0] = 0;
   while (true) {
-    const float* prow = P + (int64_t)b * p_seq_stride + (int64_t)cur * V;
+    const auto prow = src.row(b, cur);
     const float* qrow = Q ? Q + (int64_t)b * q_seq_stride + (int64_t)cur * V : nullptr;
     int accepted = -1;
     if (greedy) {
@@ -512,7 +608,7 @@ __global__ __launch_bounds__(kNT) void rejection_tree_kernel(
         const bool valid = x >= 0 && x < V;
         float cx = 0.f, qx = 1.f, px = 0.f;
         if (valid) {
-          px = prow[x];
+          px = prow.at(x);
           const float qv = res.delta ? 0.f : qrow[x];
           cx = cur_eval(res, px, qv, x);
           if (!res.delta) qx = qv;
@@ -596,10 +692,12 @@ extern "C" int nvx_temperature_softmax(const void* logits, int32_t logits_dtype,
                        logits_row_stride, temperatures, probs, vocab);
   } else if (vec && logits_dtype == NVX_DTYPE_BF16) {
     hipLaunchKernelGGL(softmax_vec_kernel<uint16_t>, dim3(num_rows), dim3(kVecNT), 0, s,
-                       (const uint16_t*)logits, logits_row_stride, temperatures, probs, vocab);
+                       (const uint16_t*)logits, logits_row_stride, temperatures, probs, vocab,
+                       (float2*)nullptr);
   } else if (vec) {
     hipLaunchKernelGGL(softmax_vec_kernel<float>, dim3(num_rows), dim3(kVecNT), 0, s,
-                       (const float*)logits, logits_row_stride, temperatures, probs, vocab);
+                       (const float*)logits, logits_row_stride, temperatures, probs, vocab,
+                       (float2*)nullptr);
   } else {
     hipLaunchKernelGGL(softmax_stream_kernel, dim3(num_rows), dim3(kNT), 0, s, logits, logits_dtype,
                        logits_row_stride, temperatures, probs, vocab);
@@ -632,10 +730,125 @@ extern "C" int nvx_rejection_sample_tree(const float* target_probs, int64_t p_se
   nvx::TimerScope timer(NVX_TIMER_REJECTION, s);
   const bool vec = vocab % 4 == 0 && p_seq_stride % 4 == 0 && aligned16(target_probs) &&
                    (draft_mode == 1 || (q_seq_stride % 4 == 0 && aligned16(draft_probs)));
-  hipLaunchKernelGGL(rejection_tree_kernel, dim3(num_seqs), dim3(kNT), 0, s, target_probs,
-                     p_seq_stride, draft_mode == 1 ? nullptr : draft_probs, q_seq_stride, vocab,
-                     tokens, parents, num_nodes, node_stride, uniforms, final_uniforms, greedy,
-                     draft_mode, path, accepted_len, out_tokens, next_token, vec);
+  hipLaunchKernelGGL(rejection_tree_kernel<ProbSource>, dim3(num_seqs), dim3(kNT), 0, s,
+                     ProbSource{target_probs, p_seq_stride, vocab},
+                     draft_mode == 1 ? nullptr : draft_probs, q_seq_stride, vocab, tokens, parents,
+                     num_nodes, node_stride, uniforms, final_uniforms, greedy, draft_mode, path,
+                     accepted_len, out_tokens, next_token, vec);
+  NVX_LAUNCHED();
+  return NVX_OK;
+}
+
+extern "C" int nvx_softmax_stats(const void* logits, int32_t logits_dtype,
+                                 int64_t logits_row_stride, const float* temperatures, float* stats,
+                                 int32_t num_rows, int32_t vocab, void* stream) {
+  nvx::clear_error();
+  NVX_CHECK(logits_dtype == NVX_DTYPE_F32 || logits_dtype == NVX_DTYPE_BF16,
+            "softmax_stats: logits must be fp32 or bf16 (dtype code %d)", logits_dtype);
+  NVX_CHECK(num_rows >= 0 && vocab >= 1 && logits_row_stride >= vocab,
+            "softmax_stats: bad sizes (rows=%d, vocab=%d, stride=%lld)", num_rows, vocab,
+            (long long)logits_row_stride);
+  if (num_rows == 0) return NVX_OK;
+  NVX_CHECK(logits && temperatures && stats, "softmax_stats: null pointer");
+  const int per = logits_dtype == NVX_DTYPE_BF16 ? 8 : 4;
+  NVX_CHECK(vocab % per == 0 && logits_row_stride % per == 0 && aligned16(logits),
+            "softmax_stats: needs 16-byte aligned logits rows with vocab and row stride "
+            "multiples of %d", per);
+  hipStream_t s = (hipStream_t)stream;
+  nvx::TimerScope timer(NVX_TIMER_SOFTMAX, s);
+  // One streaming pass (online max and sum) with four 16-byte loads in flight per
+  // thread: fewer registers, two workgroups per CU.
+  float2* st = reinterpret_cast<float2*>(stats);
+  if (logits_dtype == NVX_DTYPE_BF16)
+    hipLaunchKernelGGL((softmax_vec_kernel<uint16_t, kStatsOnly, 4>), dim3(num_rows), dim3(kVecNT),
+                       0, s, (const uint16_t*)logits, logits_row_stride, temperatures,
+                       (float*)nullptr, vocab, st);
+  else
+    hipLaunchKernelGGL((softmax_vec_kernel<float, kStatsOnly, 4>), dim3(num_rows), dim3(kVecNT), 0,
+                       s, (const float*)logits, logits_row_stride, temperatures, (float*)nullptr,
+                       vocab, st);
+  NVX_LAUNCHED();
+  return NVX_OK;
+}
+
+extern "C" int nvx_softmax_from_stats(const void* logits, int32_t logits_dtype,
+                                      int64_t logits_row_stride, const float* temperatures,
+                                      const float* stats, float* probs, int32_t num_rows,
+                                      int32_t vocab, void* stream) {
+  nvx::clear_error();
+  NVX_CHECK(logits_dtype == NVX_DTYPE_F32 || logits_dtype == NVX_DTYPE_BF16,
+            "softmax_from_stats: logits must be fp32 or bf16 (dtype code %d)", logits_dtype);
+  NVX_CHECK(num_rows >= 0 && vocab >= 1 && logits_row_stride >= vocab,
+            "softmax_from_stats: bad sizes (rows=%d, vocab=%d, stride=%lld)", num_rows, vocab,
+            (long long)logits_row_stride);
+  if (num_rows == 0) return NVX_OK;
+  NVX_CHECK(logits && temperatures && stats && probs, "softmax_from_stats: null pointer");
+  const int per = logits_dtype == NVX_DTYPE_BF16 ? 8 : 4;
+  NVX_CHECK(vocab % per == 0 && logits_row_stride % per == 0 && aligned16(logits) &&
+                aligned16(probs),
+            "softmax_from_stats: needs 16-byte aligned rows with vocab and row stride multiples "
+            "of %d", per);
+  hipStream_t s = (hipStream_t)stream;
+  nvx::TimerScope timer(NVX_TIMER_SOFTMAX, s);
+  float2* st = const_cast<float2*>(reinterpret_cast<const float2*>(stats));
+  if (logits_dtype == NVX_DTYPE_BF16)
+    hipLaunchKernelGGL((softmax_vec_kernel<uint16_t, kFromStats>), dim3(num_rows), dim3(kVecNT), 0,
+                       s, (const uint16_t*)logits, logits_row_stride, temperatures, probs, vocab, st);
+  else
+    hipLaunchKernelGGL((softmax_vec_kernel<float, kFromStats>), dim3(num_rows), dim3(kVecNT), 0, s,
+                       (const float*)logits, logits_row_stride, temperatures, probs, vocab, st);
+  NVX_LAUNCHED();
+  return NVX_OK;
+}
+
+extern "C" int nvx_rejection_sample_tree_logits(
+    const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
+    const float* temperatures, const float* stats, const float* draft_probs, int64_t q_seq_stride,
+    int32_t vocab, const int32_t* tokens, const int32_t* parents, const int32_t* num_nodes,
+    int32_t node_stride, const float* uniforms, const float* final_uniforms, const uint8_t* greedy,
+    int32_t draft_mode, int32_t num_seqs, int32_t* path, int32_t* accepted_len,
+    int32_t* out_tokens, int32_t* next_token, void* stream) {
+  nvx::clear_error();
+  NVX_CHECK(logits_dtype == NVX_DTYPE_F32 || logits_dtype == NVX_DTYPE_BF16,
+            "rejection_sample_tree_logits: logits must be fp32 or bf16 (dtype code %d)",
+            logits_dtype);
+  NVX_CHECK(num_seqs >= 0 && vocab >= 1 && logits_row_stride >= vocab,
+            "rejection_sample_tree_logits: bad sizes (seqs=%d, vocab=%d, stride=%lld)", num_seqs,
+            vocab, (long long)logits_row_stride);
+  NVX_CHECK(node_stride >= 1 && node_stride <= kMaxNodes,
+            "rejection_sample_tree_logits: node_stride must be in [1, %d] (got %d)", kMaxNodes,
+            node_stride);
+  NVX_CHECK(draft_mode == 0 || draft_mode == 1,
+            "rejection_sample_tree_logits: draft_mode must be 0 or 1");
+  NVX_CHECK(draft_mode == 1 || draft_probs != nullptr,
+            "rejection_sample_tree_logits: draft_probs required in draft_mode 0");
+  if (num_seqs == 0) return NVX_OK;
+  NVX_CHECK(logits && temperatures && stats && tokens && parents && uniforms && final_uniforms &&
+                path && accepted_len && out_tokens && next_token,
+            "rejection_sample_tree_logits: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  nvx::TimerScope timer(NVX_TIMER_REJECTION, s);
+  const bool bf16 = logits_dtype == NVX_DTYPE_BF16;
+  const uintptr_t align = bf16 ? 8 : 16;
+  const bool vec = vocab % 4 == 0 && logits_row_stride % 4 == 0 &&
+                   ((uintptr_t)logits & (align - 1)) == 0 &&
+                   (draft_mode == 1 || (q_seq_stride % 4 == 0 && aligned16(draft_probs)));
+  const float2* st = reinterpret_cast<const float2*>(stats);
+  const float* q = draft_mode == 1 ? nullptr : draft_probs;
+  if (bf16)
+    hipLaunchKernelGGL(rejection_tree_kernel<LogitSource<uint16_t>>, dim3(num_seqs), dim3(kNT), 0, s,
+                       LogitSource<uint16_t>{(const uint16_t*)logits, logits_row_stride,
+                                             node_stride, temperatures, st},
+                       q, q_seq_stride, vocab, tokens, parents, num_nodes, node_stride, uniforms,
+                       final_uniforms, greedy, draft_mode, path, accepted_len, out_tokens,
+                       next_token, vec);
+  else
+    hipLaunchKernelGGL(rejection_tree_kernel<LogitSource<float>>, dim3(num_seqs), dim3(kNT), 0, s,
+                       LogitSource<float>{(const float*)logits, logits_row_stride, node_stride,
+                                          temperatures, st},
+                       q, q_seq_stride, vocab, tokens, parents, num_nodes, node_stride, uniforms,
+                       final_uniforms, greedy, draft_mode, path, accepted_len, out_tokens,
+                       next_token, vec);
   NVX_LAUNCHED();
   return NVX_OK;
 }

@@ -43,6 +43,14 @@ _SIGS = {
                           c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_float, c_void_p],
                          c_int32),
     "nvx_silu_mul": ([c_void_p, c_int64, c_void_p, c_int32, c_int32, c_void_p], c_int32),
+    "nvx_softmax_stats": ([c_void_p, c_int32, c_int64, c_void_p, c_void_p, c_int32, c_int32,
+                           c_void_p], c_int32),
+    "nvx_softmax_from_stats": ([c_void_p, c_int32, c_int64, c_void_p, c_void_p, c_void_p, c_int32,
+                                c_int32, c_void_p], c_int32),
+    "nvx_rejection_sample_tree_logits": ([c_void_p, c_int32, c_int64, c_void_p, c_void_p, c_void_p,
+                                          c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_int32,
+                                          c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p,
+                                          c_void_p, c_void_p, c_void_p, c_void_p], c_int32),
     "nvx_topk_logprobs": ([c_void_p, c_int32, c_int64, c_int32, c_int32, c_int32, c_void_p,
                            c_void_p, c_void_p], c_int32),
     "nvx_timing_enable": ([c_int32], c_int32),

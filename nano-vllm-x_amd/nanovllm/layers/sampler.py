@@ -105,6 +105,99 @@ def rejection_sample_tree(target_probs, draft_probs, tokens, parents, uniforms, 
     return path, acc, out_tokens, nxt
 
 
+def stats_eligible(logits: torch.Tensor) -> bool:
+    """Whether logits [N, V] can take the fused path (softmax_stats and
+    rejection_sample_tree_logits): bf16 or fp32, unit stride in V, 16-byte aligned
+    rows, V and the row stride multiples of 8 (bf16) or 4 (fp32)."""
+    if logits.dim() != 2 or logits.stride(1) != 1 or logits.dtype not in _DTYPE_CODE:
+        return False
+    per = 8 if logits.dtype == torch.bfloat16 else 4
+    return (logits.shape[1] % per == 0 and logits.stride(0) % per == 0
+            and logits.data_ptr() % 16 == 0)
+
+
+def softmax_stats(logits: torch.Tensor, temperatures: torch.Tensor):
+    """Per-row softmax statistics in one streaming pass, without writing probabilities:
+    fp32 [N, 2] = (max(logits) * log2(e) / T, 1 / sum exp2(logits * log2(e) / T - max)),
+    within 1e-5 relative of the exact values; rows with T == 0 get (0, 0)."""
+    if not stats_eligible(logits):
+        raise ValueError("softmax_stats: logits must be bf16/fp32 [N, V] with 16-byte aligned rows "
+                         "and V, row stride multiples of 8 (bf16) or 4 (fp32)")
+    N, V = logits.shape
+    temperatures = temperatures.to(device=logits.device, dtype=torch.float32).contiguous()
+    if temperatures.numel() != N:
+        raise ValueError("softmax_stats: one temperature per row")
+    stats = torch.empty(N, 2, dtype=torch.float32, device=logits.device)
+    _C.require_cuda(logits, temperatures, stats)
+    _C.check(_C.lib().nvx_softmax_stats(_C.ptr(logits), _DTYPE_CODE[logits.dtype], logits.stride(0),
+                                        _C.ptr(temperatures), _C.ptr(stats), N, V,
+                                        _C.stream_of(logits)))
+    return stats
+
+
+def softmax_from_stats(logits: torch.Tensor, temperatures: torch.Tensor, stats: torch.Tensor):
+    """fp32 [N, V] probabilities exp2(fma(x, log2(e)/T, -stats[:, 0])) * stats[:, 1] (x at
+    T == 0): the values rejection_sample_tree_logits uses for the same statistics."""
+    if not stats_eligible(logits):
+        raise ValueError("softmax_from_stats: logits must be bf16/fp32 [N, V] with 16-byte aligned "
+                         "rows and V, row stride multiples of 8 (bf16) or 4 (fp32)")
+    N, V = logits.shape
+    temperatures = temperatures.to(device=logits.device, dtype=torch.float32).contiguous()
+    stats = stats.to(torch.float32).contiguous()
+    if temperatures.numel() != N or stats.shape != (N, 2):
+        raise ValueError("softmax_from_stats: one temperature and one stats row per logits row")
+    probs = torch.empty(N, V, dtype=torch.float32, device=logits.device)
+    _C.require_cuda(logits, temperatures, stats, probs)
+    _C.check(_C.lib().nvx_softmax_from_stats(_C.ptr(logits), _DTYPE_CODE[logits.dtype],
+                                             logits.stride(0), _C.ptr(temperatures), _C.ptr(stats),
+                                             _C.ptr(probs), N, V, _C.stream_of(logits)))
+    return probs
+
+
+def rejection_sample_tree_logits(logits, temperatures, stats, draft_probs, tokens, parents,
+                                 uniforms, final_uniforms, greedy=None, num_nodes=None,
+                                 draft_mode="stochastic"):
+    """rejection_sample_tree with the target rows given as logits [B*T, V] (row b*T + i
+    for node i of sequence b), their temperatures [B*T] and softmax_stats: each
+    probability the walk reads is recomputed from the logits and statistics, so the
+    results equal rejection_sample_tree(softmax_from_stats(logits, temperatures, stats))."""
+    B, T = tokens.shape
+    if not stats_eligible(logits) or logits.shape[0] != B * T:
+        raise ValueError("rejection_sample_tree_logits: logits must be [B*T, V] (see stats_eligible)")
+    V = logits.shape[1]
+    delta = draft_mode == "delta"
+    if not delta:
+        if draft_probs is None or draft_probs.dtype != torch.float32 or \
+                draft_probs.stride(2) != 1 or draft_probs.stride(1) != V or draft_probs.shape[2] != V:
+            raise ValueError("rejection_sample_tree_logits: draft_probs must be fp32 [B, T', V] "
+                             "with contiguous rows")
+    if T > 64:
+        raise ValueError("rejection_sample_tree_logits: at most 64 nodes per tree")
+    dev = logits.device
+    temperatures = temperatures.to(device=dev, dtype=torch.float32).contiguous()
+    stats = stats.to(torch.float32).contiguous()
+    if temperatures.numel() != B * T or stats.shape != (B * T, 2):
+        raise ValueError("rejection_sample_tree_logits: one temperature and one stats row per logits row")
+    tokens, parents = _i32(tokens), _i32(parents)
+    uniforms = uniforms.to(torch.float32).contiguous()
+    final_uniforms = final_uniforms.to(torch.float32).contiguous()
+    g = None if greedy is None else greedy.to(device=dev, dtype=torch.uint8).contiguous()
+    nn_ = None if num_nodes is None else _i32(num_nodes)
+    path = torch.empty(B, T, dtype=torch.int32, device=dev)
+    acc = torch.empty(B, dtype=torch.int32, device=dev)
+    out_tokens = torch.empty(B, T, dtype=torch.int32, device=dev)
+    nxt = torch.empty(B, dtype=torch.int32, device=dev)
+    _C.require_cuda(logits, temperatures, stats, draft_probs, tokens, parents, uniforms,
+                    final_uniforms, g, nn_)
+    _C.check(_C.lib().nvx_rejection_sample_tree_logits(
+        _C.ptr(logits), _DTYPE_CODE[logits.dtype], logits.stride(0), _C.ptr(temperatures),
+        _C.ptr(stats), None if delta else _C.ptr(draft_probs), 0 if delta else draft_probs.stride(0),
+        V, _C.ptr(tokens), _C.ptr(parents), _C.ptr(nn_), T, _C.ptr(uniforms), _C.ptr(final_uniforms),
+        _C.ptr(g), 1 if delta else 0, B, _C.ptr(path), _C.ptr(acc), _C.ptr(out_tokens), _C.ptr(nxt),
+        _C.stream_of(logits)))
+    return path, acc, out_tokens, nxt
+
+
 def rejection_sample_chain(target_probs, draft_probs, draft_token_ids, uniforms, final_uniforms,
                            greedy=None):
     """Chain speculative sampling (Leviathan et al. 2023, Alg. 1).
@@ -146,7 +239,9 @@ class Sampler(nn.Module):
 
 
 class RejectionSampler(nn.Module):
-    """Temperature softmax of the target logits followed by tree verification.
+    """Temperature softmax of the target logits followed by tree verification (fused
+    when the logits qualify: softmax statistics, then a walk that recomputes the
+    probabilities it reads; otherwise temperature_softmax then rejection_sample_tree).
 
     forward(target_logits [B*T, V], temperatures [B], draft_probs [B, T, V] | None,
     tokens [B, T], parents [B, T], uniforms [B, T], final_uniforms [B]) ->
@@ -158,7 +253,15 @@ class RejectionSampler(nn.Module):
         B, T = tokens.shape
         V = target_logits.shape[-1]
         temps = temperatures.to(device=target_logits.device, dtype=torch.float32)
-        probs = temperature_softmax(target_logits.view(B * T, V), temps.repeat_interleave(T))
+        rows = target_logits.view(B * T, V)
+        row_temps = temps.repeat_interleave(T)
+        mode = "delta" if draft_probs is None else "stochastic"
+        if stats_eligible(rows):
+            # fused: one statistics pass over the logits, then the walk recomputes the
+            # probabilities of the rows it visits (no fp32 probability rows written)
+            stats = softmax_stats(rows, row_temps)
+            return rejection_sample_tree_logits(rows, row_temps, stats, draft_probs, tokens, parents,
+                                                uniforms, final_uniforms, temps == 0, num_nodes, mode)
+        probs = temperature_softmax(rows, row_temps)
         return rejection_sample_tree(probs.view(B, T, V), draft_probs, tokens, parents, uniforms,
-                                     final_uniforms, temps == 0, num_nodes,
-                                     "delta" if draft_probs is None else "stochastic")
+                                     final_uniforms, temps == 0, num_nodes, mode)

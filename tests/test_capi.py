@@ -48,6 +48,12 @@ def test_validation_errors_are_reported():
     assert rc == -1 and b"k must be" in lib.nvx_last_error()
     rc = lib.nvx_topk_logprobs(None, _C.DTYPE_BF16, 100, 1, 100, 8, None, None, None)
     assert rc == -1 and b"multiples of 8" in lib.nvx_last_error()
+    rc = lib.nvx_softmax_stats(None, _C.DTYPE_BF16, 100, None, None, 1, 100, None)
+    assert rc == -1 and b"null pointer" in lib.nvx_last_error()
+    rc = lib.nvx_rejection_sample_tree_logits(None, _C.DTYPE_BF16, 64, None, None, None, 0, 64, None,
+                                              None, None, 65, None, None, None, 1, 1, None, None,
+                                              None, None, None)
+    assert rc == -1 and b"node_stride" in lib.nvx_last_error()
 
 
 def test_workspace_size_plan():

@@ -7,7 +7,9 @@ import numpy as np
 import pytest
 import torch
 
-from nanovllm.layers.sampler import (Sampler, rejection_sample_chain, rejection_sample_tree,
+from nanovllm.layers.sampler import (RejectionSampler, Sampler, rejection_sample_chain,
+                                     rejection_sample_tree, rejection_sample_tree_logits,
+                                     softmax_from_stats, softmax_stats, stats_eligible,
                                      temperature_softmax)
 from nanovllm.spec.tree import chain_parents, random_tree
 from oracle import sampler as osamp
@@ -183,3 +185,102 @@ def test_sampler_distribution(dev):
     assert chi2 < 40.0, chi2  # 11 dof: p(chi2 > 40) ~ 3e-5
     tg = Sampler()(logits[:8].to(dev), torch.zeros(8).to(dev)).cpu().numpy()
     assert (tg == V - 1).all()
+
+
+def fused_case(dev, B, T, V, depth, seed, dtype=torch.bfloat16, delta=False, greedy_frac=0.0,
+               temp=0.8):
+    """Fused sampler (softmax_stats + rejection_sample_tree_logits) against the walk on
+    the probabilities softmax_from_stats materialises from the same statistics, on the
+    GPU and in the oracle: bit-exact integer outputs.  Those probabilities match
+    temperature_softmax within 1e-5.  Draft rows are close to the target rows, so walks
+    go deep and read many rows."""
+    rng = np.random.default_rng(seed)
+    g = torch.Generator().manual_seed(seed)
+    logits = (torch.randn(B * T, V, generator=g) * 2).to(dtype)
+    greedy = rng.random(B) < greedy_frac
+    temps = torch.where(torch.from_numpy(greedy), torch.tensor(0.0), torch.tensor(temp))
+    row_temps = temps.repeat_interleave(T)
+    Q = torch.softmax((logits.float() + 0.3 * torch.randn(B * T, V, generator=g)) / temp, -1).view(B, T, V)
+    parents = np.stack([random_tree(T, depth, rng) for _ in range(B)])
+    toks = np.zeros((B, T), np.int32)
+    Qn = Q.numpy()
+    for b in range(B):
+        for i in range(1, T):
+            row = Qn[b, parents[b, i]].astype(np.float64)
+            toks[b, i] = min(int(np.searchsorted(np.cumsum(row), rng.random() * row.sum())), V - 1)
+    U = torch.from_numpy(rng.random((B, T)).astype(np.float32))
+    Uf = torch.from_numpy(rng.random(B).astype(np.float32))
+    mode = "delta" if delta else "stochastic"
+    print(f"[fused] B={B} T={T} V={V} dtype={dtype} mode={mode} seed={seed}", flush=True)
+    ld, rtd = logits.to(dev), row_temps.to(dev)
+    assert stats_eligible(ld)
+    args = (None if delta else Q.to(dev), torch.from_numpy(toks).to(dev),
+            torch.from_numpy(parents).to(dev), U.to(dev), Uf.to(dev),
+            torch.from_numpy(greedy).to(dev), None, mode)
+    stats = softmax_stats(ld, rtd)
+    fused = rejection_sample_tree_logits(ld, rtd, stats, *args)
+    P = softmax_from_stats(ld, rtd, stats)
+    np.testing.assert_allclose(P.cpu().numpy(), temperature_softmax(ld, rtd).cpu().numpy(),
+                               rtol=1e-5, atol=1e-35)
+    two = rejection_sample_tree(P.view(B, T, V), *args)
+    ref = osamp.rejection_sample_tree(P.cpu().numpy().reshape(B, T, V), None if delta else Qn, toks,
+                                      parents, U.numpy(), Uf.numpy(), greedy, None, delta)
+    names = ("path", "accepted_len", "out_tokens", "next_token")
+    for name, a, b_, r in zip(names, fused, two, ref):
+        assert np.array_equal(a.cpu().numpy(), b_.cpu().numpy()), f"{name}: fused != walk on P"
+        assert np.array_equal(a.cpu().numpy(), r), f"{name}: fused != oracle"
+    # statistics against the float64 softmax (1e-5 relative)
+    x = logits.float().numpy().astype(np.float64)
+    live = row_temps.numpy() > 0
+    a = 1.4426950408889634 / np.where(live, row_temps.numpy(), 1.0)
+    M = x.max(1) * a
+    S = np.exp2(x * a[:, None] - M[:, None]).sum(1)
+    st = stats.cpu().numpy()
+    np.testing.assert_allclose(st[live, 0], M[live], rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(st[live, 1], 1.0 / S[live], rtol=1e-5)
+    assert (st[~live] == 0).all()
+    return fused
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("V,dtype", [(V_QWEN, torch.bfloat16), (128256, torch.bfloat16),
+                                     (1000, torch.bfloat16), (4096, torch.float32)])
+def test_fused_sampler_matches_two_step(dev, V, dtype):
+    """Both register-resident size classes (38 and 32 groups), the streaming kernel for
+    bf16 and fp32; sampled and greedy sequences in one batch."""
+    fused_case(dev, B=6, T=24, V=V, depth=5, seed=V % 97, dtype=dtype, greedy_frac=0.3)
+
+
+@pytest.mark.gpu
+def test_fused_sampler_delta_and_deep_trees(dev):
+    fused_case(dev, B=4, T=64, V=V_QWEN, depth=8, seed=11, delta=True)
+    acc = fused_case(dev, B=8, T=64, V=2048, depth=20, seed=12)[1]
+    assert int(acc.max()) >= 3  # close draft rows: walks go several levels deep
+
+
+@pytest.mark.gpu
+def test_rejection_sampler_module_paths(dev):
+    """RejectionSampler takes the fused path for eligible logits (equal to the walk on
+    softmax_from_stats) and the two-step path otherwise (equal to the walk on
+    temperature_softmax)."""
+    for V in (4096, 1001):  # 1001: not a multiple of 8, two-step path
+        rng = np.random.default_rng(V)
+        g = torch.Generator().manual_seed(V)
+        B, T = 5, 12
+        logits = (torch.randn(B * T, V, generator=g) * 2).to(torch.bfloat16).to(dev)
+        Q = torch.softmax(torch.randn(B, T, V, generator=g), -1).to(dev)
+        parents = torch.from_numpy(np.stack([random_tree(T, 4, rng) for _ in range(B)])).to(dev)
+        toks = torch.from_numpy(rng.integers(0, V, size=(B, T)).astype(np.int32)).to(dev)
+        U = torch.from_numpy(rng.random((B, T)).astype(np.float32)).to(dev)
+        Uf = torch.from_numpy(rng.random(B).astype(np.float32)).to(dev)
+        temps = torch.tensor([0.7, 0.0, 1.0, 1.3, 0.9], device=dev)
+        assert stats_eligible(logits) == (V == 4096)
+        got = RejectionSampler()(logits, temps, Q, toks, parents, U, Uf)
+        rt = temps.repeat_interleave(T)
+        if V == 4096:
+            P = softmax_from_stats(logits, rt, softmax_stats(logits, rt)).view(B, T, V)
+        else:
+            P = temperature_softmax(logits, rt).view(B, T, V)
+        want = rejection_sample_tree(P, Q, toks, parents, U, Uf, temps == 0)
+        for a, b_ in zip(got, want):
+            assert torch.equal(a, b_)
