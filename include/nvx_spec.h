@@ -170,7 +170,8 @@ int nvx_rejection_sample_tree(const float* target_probs, int64_t p_seq_stride,
  *   pass gives stats[2r] = max_y(logit[y]) * log2(e)/T and stats[2r+1] = 1 / sum_y
  *   exp2(logit[y] * log2(e)/T - stats[2r]) (fp32, within 1e-5 relative of the exact
  *   values); T == 0 rows get (0, 0).  Logits rows must be 16-byte aligned with vocab
- *   and row stride multiples of 8 (bf16) or 4 (fp32).
+ *   and row stride multiples of 8 (bf16) or 4 (fp32).  stats is [num_rows, 2] fp32,
+ *   8-byte aligned (all three entry points check this).
  * nvx_softmax_from_stats: probs[r][y] = exp2(fma(logit[y], log2(e)/T, -stats[2r])) *
  *   stats[2r+1], or logit[y] when T == 0: the probabilities the fused walk uses (same
  *   alignment rules; probs 16-byte aligned, [num_rows, vocab] contiguous).

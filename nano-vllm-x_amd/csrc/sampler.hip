@@ -666,6 +666,8 @@ __global__ __launch_bounds__(kNT) void rejection_tree_kernel(
 }
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+// The row statistics are read and written as float2 (max, 1/sum) pairs.
+inline bool aligned8(const void* p) { return ((uintptr_t)p & 7) == 0; }
 
 }  // namespace
 
@@ -750,6 +752,7 @@ extern "C" int nvx_softmax_stats(const void* logits, int32_t logits_dtype,
             (long long)logits_row_stride);
   if (num_rows == 0) return NVX_OK;
   NVX_CHECK(logits && temperatures && stats, "softmax_stats: null pointer");
+  NVX_CHECK(aligned8(stats), "softmax_stats: stats must be 8-byte aligned");
   const int per = logits_dtype == NVX_DTYPE_BF16 ? 8 : 4;
   NVX_CHECK(vocab % per == 0 && logits_row_stride % per == 0 && aligned16(logits),
             "softmax_stats: needs 16-byte aligned logits rows with vocab and row stride "
@@ -783,6 +786,7 @@ extern "C" int nvx_softmax_from_stats(const void* logits, int32_t logits_dtype,
             (long long)logits_row_stride);
   if (num_rows == 0) return NVX_OK;
   NVX_CHECK(logits && temperatures && stats && probs, "softmax_from_stats: null pointer");
+  NVX_CHECK(aligned8(stats), "softmax_from_stats: stats must be 8-byte aligned");
   const int per = logits_dtype == NVX_DTYPE_BF16 ? 8 : 4;
   NVX_CHECK(vocab % per == 0 && logits_row_stride % per == 0 && aligned16(logits) &&
                 aligned16(probs),
@@ -826,6 +830,7 @@ extern "C" int nvx_rejection_sample_tree_logits(
   NVX_CHECK(logits && temperatures && stats && tokens && parents && uniforms && final_uniforms &&
                 path && accepted_len && out_tokens && next_token,
             "rejection_sample_tree_logits: null pointer");
+  NVX_CHECK(aligned8(stats), "rejection_sample_tree_logits: stats must be 8-byte aligned");
   hipStream_t s = (hipStream_t)stream;
   nvx::TimerScope timer(NVX_TIMER_REJECTION, s);
   const bool bf16 = logits_dtype == NVX_DTYPE_BF16;

@@ -50,6 +50,12 @@ def test_validation_errors_are_reported():
     assert rc == -1 and b"multiples of 8" in lib.nvx_last_error()
     rc = lib.nvx_softmax_stats(None, _C.DTYPE_BF16, 100, None, None, 1, 100, None)
     assert rc == -1 and b"null pointer" in lib.nvx_last_error()
+    # Non-null host addresses: each call is refused before anything is launched.
+    rows, stats = ctypes.c_void_p(0x100000), ctypes.c_void_p(0x200004)
+    rc = lib.nvx_softmax_stats(rows, _C.DTYPE_BF16, 128, rows, stats, 1, 128, None)
+    assert rc == -1 and b"8-byte aligned" in lib.nvx_last_error()
+    rc = lib.nvx_softmax_from_stats(rows, _C.DTYPE_BF16, 128, rows, stats, rows, 1, 128, None)
+    assert rc == -1 and b"8-byte aligned" in lib.nvx_last_error()
     rc = lib.nvx_rejection_sample_tree_logits(None, _C.DTYPE_BF16, 64, None, None, None, 0, 64, None,
                                               None, None, 65, None, None, None, 1, 1, None, None,
                                               None, None, None)
