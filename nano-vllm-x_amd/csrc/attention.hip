@@ -71,15 +71,29 @@ __device__ __forceinline__ uint16_t f2bf(float x) {
 // so both read patterns are bank-conflict free.
 __device__ __forceinline__ int swz(int row) { return ((row & 3) << 2) | ((row >> 2) & 3); }
 
+// Cache policy of the K/V loads.  kShared: the K/V of a (sequence, KV head) is read
+// by several workgroups (one per q-row chunk), which meet in L2; the loads skip the
+// vector L1 (sc1), where nothing is reused.  kStream: every K/V byte is read once
+// (one q-row chunk), so the loads are non-temporal (nt) and do not displace what
+// other work keeps in the caches.
+enum DmaPolicy { kShared = 0, kStream = 1 };
+
 // Wave-wide 16-byte-per-lane load from global memory straight into LDS: lane i's
 // data lands at LDS byte address lds_base + 16*i.  Issued from inline asm so the
 // compiler does not fence every LDS read behind it; completion is waited for
 // explicitly with wait_vm below (each call counts one vector-memory op per wave).
+template <int kPolicy>
 __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
-               :
-               : "v"(voff), "s"(sbase), "s"(lds_base)
-               : "memory", "m0");
+  if constexpr (kPolicy == kStream)
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds_base)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 sc1"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds_base)
+                 : "memory", "m0");
 }
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -102,7 +116,7 @@ __device__ __forceinline__ int remap_xcd(int phys, int n) {
 }
 
 // Two waves per SIMD (at most 256 VGPR+AGPR each): two 4-wave workgroups per CU.
-template <int W>
+template <int W, int kPolicy>
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void tree_attn_kernel(AttnParams p) {
   constexpr int PER = kDmaPerChunk / W;  // LDS-DMA loads per wave per chunk
@@ -207,7 +221,7 @@ void tree_attn_kernel(AttnParams p) {
     for (int j = 0; j < PER; ++j) {
       const int ii = wave + W * j;
       const int row = full || pos0 + lane_row[j] < ctxlen ? lane_row[j] : 0;
-      dma16(ii >> 4 ? vbase : kbase, lane_off[j] + (uint32_t)(row * row_stride),
+      dma16<kPolicy>(ii >> 4 ? vbase : kbase, lane_off[j] + (uint32_t)(row * row_stride),
             ring_base + st * kStageBytes + (ii >> 4) * kTileBytes + (ii & 15) * 1024);
     }
   };
@@ -554,7 +568,15 @@ extern "C" int nvx_tree_attention(const void* q, void* o, const void* k_cache, c
   const int64_t nblocks = (int64_t)num_seqs * num_kv_heads * pl.nq * pl.nsplit;
   NVX_CHECK(nblocks < (1ll << 31), "tree_attention: grid too large");
   const dim3 grid((unsigned)nblocks);
-  hipLaunchKernelGGL(tree_attn_kernel<kWaves>, grid, dim3(kWaves * 64), 0, s, p);
+  // One q-row chunk per (sequence, KV head): K/V is streamed once (32 sequences of
+  // 32-node trees over 1-4k keys, 16/8 heads: 85 us against 93 us with cached loads;
+  // decode of 64 x 2k keys: 89 us against 102 us).  Two or more chunks share K/V
+  // through L2, which non-temporal loads would give up (64 sequences of 64-node trees
+  // over 2k keys, 32/8 heads: 220 us against 202 us with sc1 loads).
+  if (pl.nq == 1)
+    hipLaunchKernelGGL((tree_attn_kernel<kWaves, kStream>), grid, dim3(kWaves * 64), 0, s, p);
+  else
+    hipLaunchKernelGGL((tree_attn_kernel<kWaves, kShared>), grid, dim3(kWaves * 64), 0, s, p);
   NVX_LAUNCHED();
   if (pl.nsplit > 1) {
     hipLaunchKernelGGL(combine_kernel, dim3(total_q * num_heads), dim3(kD), 0, s, p.part_o,
