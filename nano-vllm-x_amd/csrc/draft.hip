@@ -128,7 +128,7 @@ __global__ __launch_bounds__(NT) void topk_logprobs_kernel(const VT* __restrict_
     const int i = j + lane;
     uint4 w[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) w[u] = src[i + u * NT];
+    for (int u = 0; u < kUnroll; ++u) w[u] = nvx::ld_stream(src + i + u * NT);
     float x[kUnroll][P];
     float lm = -INFINITY;
 #pragma unroll

@@ -98,7 +98,8 @@ __global__ __launch_bounds__(kNT) void kv_compact_kernel(
       u32x4 rows[kDepthGroup];
 #pragma unroll
       for (int j = 0; j < kDepthGroup; ++j)
-        rows[j] = *reinterpret_cast<const u32x4*>(base + max(src[j], (int64_t)0) * row_bytes);
+        rows[j] = __builtin_nontemporal_load(  // each accepted row is read once
+            reinterpret_cast<const u32x4*>(base + max(src[j], (int64_t)0) * row_bytes));
 #pragma unroll
       for (int j = 0; j < kDepthGroup; ++j)
         if (src[j] >= 0 && dst[j] >= 0) *reinterpret_cast<u32x4*>(base + dst[j] * row_bytes) = rows[j];

@@ -51,6 +51,17 @@ __device__ __forceinline__ float shfl_xor_f(float v, int off) { return __shfl_xo
 __device__ __forceinline__ int shfl_xor_i(int v, int off) { return __shfl_xor(v, off, 64); }
 __device__ __forceinline__ float shfl_up_f(float v, int off) { return __shfl_up(v, off, 64); }
 
+// 16-byte load with the non-temporal hint (`global_load_dwordx4 ... nt`), for data a
+// kernel streams from HBM exactly once: the softmax statistics pass over [4096, 151936]
+// bf16 logits takes 180 us with it against 207 us without, top-k 116 against 123 us.
+// Not for inputs the previous kernel has just written (the fused layers after a GEMM
+// measured the same or slower with it).
+__device__ __forceinline__ uint4 ld_stream(const void* p) {
+  typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+  const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 

@@ -90,7 +90,8 @@ __global__ __launch_bounds__(kVecNT) void softmax_vec_kernel(const VT* __restric
     for (; i + (kUnroll - 1) * kVecNT < nvec; i += kUnroll * kVecNT) {
       uint4 w[kUnroll];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) w[u] = src[i + u * kVecNT];
+      for (int u = 0; u < kUnroll; ++u)
+        w[u] = kMode == kStatsOnly ? nvx::ld_stream(src + i + u * kVecNT) : src[i + u * kVecNT];
       float lm = -INFINITY;
       float x[kUnroll][P];
 #pragma unroll
