@@ -49,9 +49,12 @@ def test_rmsnorm_plain_and_add(dev, H):
 
 
 @pytest.mark.gpu
-def test_qk_norm_rope(dev):
-    g = torch.Generator().manual_seed(0)
-    N, Hq, Hkv, D = 300, 8, 2, 128
+# Head layouts of Qwen3-8B (32/8) and Qwen3-0.6B (16/8) and two others, with token
+# counts that leave a partial last workgroup.
+@pytest.mark.parametrize("N,Hq,Hkv", [(300, 8, 2), (301, 32, 8), (77, 16, 8), (50, 12, 4)])
+def test_qk_norm_rope(dev, N, Hq, Hkv):
+    g = torch.Generator().manual_seed(N)
+    D = 128
     qkv = torch.randn(N, (Hq + 2 * Hkv) * D, generator=g).to(torch.bfloat16)
     qw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
     kw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
