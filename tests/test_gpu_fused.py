@@ -30,7 +30,8 @@ def ulps(a, b):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("H", [4096, 1024, 128])
+# Hidden sizes of the Qwen3 family and two others, 257 rows each.
+@pytest.mark.parametrize("H", [4096, 3072, 2048, 1024, 1536, 128])
 def test_rmsnorm_plain_and_add(dev, H):
     g = torch.Generator().manual_seed(H)
     x = torch.randn(257, H, generator=g).to(torch.bfloat16)
