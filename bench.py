@@ -58,6 +58,9 @@ def parse():
                     help="sequences in the CPU-baseline sample (0 disables it)")
     ap.add_argument("--parity-seqs", type=int, default=8,
                     help="sequences of the integrated step checked against the oracle (0: off)")
+    ap.add_argument("--small-tree-attention", action=argparse.BooleanOptionalAction, default=True,
+                    help="also time tree attention at the Qwen3-0.6B shape (batch 32, 32-node "
+                         "trees, ctx 1024-4096) with a parity check on 2 sequences")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device copy (HBM counter calibration)")
     ap.add_argument("--workload", choices=("verify", "e2e", "kernels"), default="verify")
@@ -217,17 +220,24 @@ def build_step(args, torch, dev):
     ugen = torch.Generator(device=dev).manual_seed(args.seed + 2)
 
     @torch.inference_mode()
-    def step(capture=None):
-        """One verify step; returns [B, 1 + T] int32 on the host: accepted_len, then
-        the path.  capture (a dict, outside the timed region) receives the step's
-        logits, uniforms and sampler outputs, and a copy of the KV cache from before
-        the compaction, for the parity check."""
+    def forward():
+        """The target forward over the tree rows and the LM head: logits [B*T, V]."""
         set_context(False, cu_seqlens_q=cu_q, slot_mapping=slot_mapping, context_lens=context_lens,
                     block_tables=block_tables, tree_mask=tree_mask, max_seqlen_q=T,
                     max_context_len=int(vb.context_lens.max()))
         hidden = model(input_ids, positions)
         logits = model.compute_logits(hidden)
         reset_context()
+        return logits
+
+    @torch.inference_mode()
+    def step(capture=None):
+        """One verify step; returns [B, 1 + T] int32 on the host: accepted_len, then
+        the path.  capture (a dict, outside the timed region) receives the step's
+        logits, uniforms and sampler outputs, and a copy of the KV cache from before
+        the compaction, for the parity check.  Raises if the walk failed for any
+        sequence (accepted_len -1)."""
+        logits = forward()
         U = torch.rand(B, T, device=dev, generator=ugen)
         Uf = torch.rand(B, device=dev, generator=ugen)
         path, acc, out_tok, nxt = sampler(logits, temps, Q, tokens32, parents, U, Uf)
@@ -236,10 +246,14 @@ def build_step(args, torch, dev):
             capture.update(logits=logits, U=U, Uf=Uf, path=path, acc=acc, out_tokens=out_tok,
                            next_token=nxt, kv_before=kv_cache[:, lay][:, :, pages].clone())
         kv_compact(kv_cache[0], kv_cache[1], block_tables, ctx, path, acc)
-        return torch.cat([acc[:, None], path], dim=1).cpu()
+        res = torch.cat([acc[:, None], path], dim=1).cpu()
+        if bool((res[:, 0] < 0).any()):
+            raise RuntimeError("tree rejection walk failed (accepted_len -1) for batch rows "
+                               f"{torch.nonzero(res[:, 0] < 0).flatten().tolist()}")
+        return res
 
-    state = dict(model=model, kv_cache=kv_cache, vb=vb, Q=Q, tokens=tokens32, parents=parents,
-                 cfg=cfg, temps=temps)
+    state = dict(model=model, kv_cache=kv_cache, vb=vb, Q=Q, tokens=tokens32, tokens64=tokens,
+                 parents=parents, cfg=cfg, temps=temps, forward=forward)
     return step, state
 
 
@@ -348,14 +362,62 @@ def cpu_baseline(args, torch, state, nseq):
     return float((acc + 1).sum()) / dt, cores, dt
 
 
+def plant_greedy_spines(torch, state, nplant, depth):
+    """Make the first nplant sequences greedy (temperature 0) and plant, along the
+    root-to-leaf path to each tree's first deepest node, the target's own greedy
+    chain: the token of the path's node d is the argmax of the target row of node
+    d - 1.  A row depends on the tokens of its ancestors, so the chain is built depth
+    by depth, one target forward per depth.  Then the greedy walk accepts the whole
+    path (accepted_len = depth, unless an earlier sibling carries the same token or
+    the argmax is tied) and compaction moves depth rows in every layer.  Returns the
+    planted paths and a function that restores the tokens and temperatures."""
+    import numpy as np
+    from nanovllm.spec.tree import depths as tree_depths
+
+    tok64, tok32, temps = state["tokens64"], state["tokens"], state["temps"]
+    saved = (tok64.clone(), temps.clone())
+    T = tok64.shape[1]
+    parents = state["parents"].cpu().numpy()
+    paths = []
+    for b in range(nplant):
+        d = tree_depths(parents[b])
+        node = int(np.argmax(d))
+        path = [node]
+        while path[-1] != 0:
+            path.append(int(parents[b][path[-1]]))
+        paths.append(path[::-1])
+    temps[:nplant] = 0.0
+    with torch.inference_mode():
+        for lvl in range(1, 1 + min([depth] + [len(p) - 1 for p in paths]) if paths else 1):
+            logits = state["forward"]()
+            rows = torch.tensor([b * T + p[lvl - 1] for b, p in enumerate(paths)],
+                                device=logits.device)
+            am = logits[rows].float().argmax(-1)
+            for b, p in enumerate(paths):
+                tok64[b, p[lvl]] = am[b]
+            tok32.copy_(tok64.to(torch.int32))
+    torch.cuda.synchronize()
+
+    def restore():
+        tok64.copy_(saved[0])
+        tok32.copy_(saved[0].to(torch.int32))
+        temps.copy_(saved[1])
+
+    return paths, restore
+
+
 def integrated_parity(args, torch, state, step, nseq):
     """One more verify step (outside the timed region), checked against the oracle on
-    the step's own data for its first nseq sequences: the oracle walks the
-    probabilities of the GPU's logits (nvx_softmax_from_stats with the statistics the
-    sampler used, themselves checked against the float64 softmax) with the same draft
-    rows, tokens, tree and uniforms, and compacts a copy of the pre-compaction KV pages
-    of the first and last layer along the GPU's paths.  Integer outputs and KV bytes
-    must be equal.  Returns the parity record."""
+    the step's own data for its first nseq sequences.  The first half of them are
+    made greedy with the target's own greedy chain planted on a root-to-leaf path
+    (plant_greedy_spines), so the walk accepts deep paths and compaction moves that
+    many rows in all layers; the rest stay stochastic at the bench temperature.  The
+    oracle walks the probabilities of the GPU's logits (nvx_softmax_from_stats with
+    the statistics the sampler used, themselves checked against the float64 softmax;
+    the fp32 logits for greedy rows) with the same draft rows, tokens, tree and
+    uniforms, and compacts a copy of the pre-compaction KV pages of the first and last
+    layer along the GPU's paths.  Integer outputs and KV bytes must be equal.  Returns
+    the parity record."""
     import numpy as np
     from nanovllm.layers.sampler import softmax_from_stats, softmax_stats
     from oracle import kvcache as okv, sampler as osamp
@@ -363,39 +425,55 @@ def integrated_parity(args, torch, state, step, nseq):
     vb, cfg, kv = state["vb"], state["cfg"], state["kv_cache"]
     B, T, V, L = args.batch, args.tree_nodes, cfg.vocab_size, cfg.num_hidden_layers
     dev = kv.device
-    used = sorted({int(x) for b in range(nseq) for x in vb.bt[b] if x >= 0})
-    remap = {old: i for i, old in enumerate(used)}
-    bt_local = np.array([[remap.get(int(x), -1) for x in vb.bt[b]] for b in range(nseq)], np.int32)
-    layers = [0, L - 1]
-    cap = {"kv_layers": torch.tensor(layers, device=dev), "kv_pages": torch.tensor(used, device=dev)}
-    step(capture=cap)
-    torch.cuda.synchronize()
-    rows = cap["logits"][:nseq * T]
-    rtemps = torch.full((nseq * T,), args.temperature, device=dev)
-    stats = softmax_stats(rows, rtemps)
-    P = softmax_from_stats(rows, rtemps, stats).cpu().numpy()
-    Pref = osamp.temperature_softmax(rows.float().cpu().numpy(), rtemps.cpu().numpy())
-    softmax_ok = bool(np.allclose(P, Pref, rtol=1e-5, atol=1e-35))
-    gpu = {k: cap[k][:nseq].cpu().numpy() for k in ("path", "acc", "out_tokens", "next_token")}
-    ref_path, ref_acc, ref_tok, ref_next = osamp.rejection_sample_tree(
-        P.reshape(nseq, T, V), state["Q"][:nseq].cpu().numpy(), state["tokens"][:nseq].cpu().numpy(),
-        state["parents"][:nseq].cpu().numpy(), cap["U"][:nseq].cpu().numpy(),
-        cap["Uf"][:nseq].cpu().numpy(), np.zeros(nseq, bool))
-    # KV compaction of the sampled sequences' pages, layers 0 and L-1
-    as_u16 = lambda t: t.view(torch.int16).cpu().numpy().view(np.uint16)  # noqa: E731
-    before = as_u16(cap["kv_before"])                    # [2, 2 layers, pages, bs, Hkv, D]
-    after = as_u16(kv[:, cap["kv_layers"]][:, :, cap["kv_pages"]])
-    k_ref, v_ref = before[0].copy(), before[1].copy()
-    okv.kv_compact(k_ref, v_ref, bt_local, vb.ctx[:nseq], gpu["path"], gpu["acc"], 256)
-    kv_ok = bool(np.array_equal(after[0], k_ref) and np.array_equal(after[1], v_ref))
+    nplant = nseq // 2
+    paths, restore = plant_greedy_spines(torch, state, nplant, args.tree_depth)
+    try:
+        used = sorted({int(x) for b in range(nseq) for x in vb.bt[b] if x >= 0})
+        remap = {old: i for i, old in enumerate(used)}
+        bt_local = np.array([[remap.get(int(x), -1) for x in vb.bt[b]] for b in range(nseq)],
+                            np.int32)
+        layers = [0, L - 1]
+        cap = {"kv_layers": torch.tensor(layers, device=dev),
+               "kv_pages": torch.tensor(used, device=dev)}
+        step(capture=cap)
+        torch.cuda.synchronize()
+        rows = cap["logits"][:nseq * T]
+        seq_temps = state["temps"][:nseq].clone()
+        rtemps = seq_temps.repeat_interleave(T)
+        stats = softmax_stats(rows, rtemps)
+        P = softmax_from_stats(rows, rtemps, stats).cpu().numpy()
+        Pref = osamp.temperature_softmax(rows.float().cpu().numpy(), rtemps.cpu().numpy())
+        softmax_ok = bool(np.allclose(P, Pref, rtol=1e-5, atol=1e-35))
+        greedy = seq_temps.cpu().numpy() == 0
+        gpu = {k: cap[k][:nseq].cpu().numpy() for k in ("path", "acc", "out_tokens", "next_token")}
+        ref_path, ref_acc, ref_tok, ref_next = osamp.rejection_sample_tree(
+            P.reshape(nseq, T, V), state["Q"][:nseq].cpu().numpy(),
+            state["tokens"][:nseq].cpu().numpy(), state["parents"][:nseq].cpu().numpy(),
+            cap["U"][:nseq].cpu().numpy(), cap["Uf"][:nseq].cpu().numpy(), greedy)
+        # KV compaction of the sampled sequences' pages, layers 0 and L-1
+        as_u16 = lambda t: t.view(torch.int16).cpu().numpy().view(np.uint16)  # noqa: E731
+        before = as_u16(cap["kv_before"])                    # [2, 2 layers, pages, bs, Hkv, D]
+        after = as_u16(kv[:, cap["kv_layers"]][:, :, cap["kv_pages"]])
+        k_ref, v_ref = before[0].copy(), before[1].copy()
+        okv.kv_compact(k_ref, v_ref, bt_local, vb.ctx[:nseq], gpu["path"], gpu["acc"], 256)
+        kv_ok = bool(np.array_equal(after[0], k_ref) and np.array_equal(after[1], v_ref))
+        moved = int(np.clip(gpu["acc"], 0, None).sum())
+    finally:
+        restore()
     return {"path": bool(np.array_equal(gpu["path"], ref_path)),
             "accepted_len": bool(np.array_equal(gpu["acc"], ref_acc)),
             "tokens": bool(np.array_equal(gpu["out_tokens"], ref_tok)),
             "next_token": bool(np.array_equal(gpu["next_token"], ref_next)),
             "kv_compact": kv_ok, "softmax_within_1e-5": softmax_ok,
             "accepted": [int(a) for a in gpu["acc"]],
-            "sample": f"first {nseq} of {B} sequences of one more verify step; KV of layers "
-                      f"{layers[0]} and {layers[1]}"}
+            "greedy": [bool(g) for g in greedy],
+            "planted_path_len": [len(p) - 1 for p in paths],
+            "kv_rows_moved_per_layer": moved,
+            "sample": f"first {nseq} of {B} sequences of one more verify step, the first "
+                      f"{nplant} greedy with the target's greedy chain planted on a "
+                      f"root-to-leaf path ({max([0] + [len(p) - 1 for p in paths])} extra target "
+                      f"forwards before it, untimed), the rest stochastic at T = {args.temperature}; KV "
+                      f"of layers {layers[0]} and {layers[1]}"}
 
 
 def walk_rows(parents, path_acc):
@@ -418,6 +496,67 @@ def walk_rows(parents, path_acc):
             p_rows += rej + (1 if d == acc and rej == 0 else 0)
             q_rows += rej
     return p_rows, q_rows
+
+
+def gpu_launch_us(torch, fn, timer, iters=20, warm=3):
+    """Average µs per launch of the library kernel `timer` over `iters` calls of fn
+    (after `warm` untimed calls), from the library's HIP events on the launch stream."""
+    from nanovllm import _C
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    _C.timing_reset()
+    _C.timing_enable(True)
+    for _ in range(iters):
+        fn()
+    torch.cuda.synchronize()
+    _C.timing_enable(False)
+    ms, n = _C.timing_read(timer)
+    return ms / n * 1e3
+
+
+def attention_small_tree(torch, dev, seed, gpu_us, check_seqs):
+    """Tree attention at the Qwen3-0.6B shape (16/8 heads, d 128): 32 sequences with
+    1024-4096 cached tokens and 32-node depth-6 trees in randomly scattered 256-token
+    pages.  Times the launch (split-KV main kernel and merge) with the library's
+    HIP-event timer and checks the first check_seqs sequences against the oracle
+    (2e-2 absolute).  Returns a record."""
+    import numpy as np
+    from nanovllm import _C
+    from nanovllm.layers.attention import tree_attention
+    from nanovllm.utils.synthetic import VerifyBatch
+    from oracle import attention as oatt
+
+    B, T, Hq, Hkv, D = 32, 32, 16, 8, 128
+    rng = np.random.default_rng(seed + 2)
+    vb = VerifyBatch.random(B, (1024, 4096), T, 6, 256, rng)
+    g = torch.Generator().manual_seed(seed + 2)
+    kc = (torch.randn(vb.num_blocks, 256, Hkv, D, generator=g)).to(torch.bfloat16)
+    vc = (torch.randn(vb.num_blocks, 256, Hkv, D, generator=g)).to(torch.bfloat16)
+    N = int(vb.cu_q[-1])
+    q = torch.randn(N, Hq, D, generator=g).to(torch.bfloat16)
+    t = lambda a, dt=torch.int32: torch.from_numpy(a).to(dev, dt)  # noqa: E731
+    qd, kcd, vcd = q.to(dev), kc.to(dev), vc.to(dev)
+    a_args = (qd, kcd, vcd, t(vb.bt), t(vb.cu_q), t(vb.context_lens), D ** -0.5,
+              t(vb.masks, torch.int64), T, int(vb.context_lens.max()))
+    us = gpu_us(lambda: tree_attention(*a_args), _C.TIMER_TREE_ATTENTION)
+    o = tree_attention(*a_args).float().cpu().numpy()
+    ns = check_seqs
+    rows = int(vb.cu_q[ns])
+    t0 = time.perf_counter()
+    ref = oatt.paged_attention(
+        q[:rows].float().numpy(), kc.float().numpy(), vc.float().numpy(), vb.bt[:ns],
+        vb.cu_q[:ns + 1], vb.context_lens[:ns], vb.masks[:rows].view(np.uint64), D ** -0.5, 256)
+    cus = (time.perf_counter() - t0) * 1e6
+    err = float(np.abs(o[:rows] - ref).max())
+    nbytes = float(vb.context_lens.sum()) * Hkv * D * 2 * 2 + 2.0 * N * Hq * D * 2
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"config": "Qwen3-0.6B shape (16/8 heads, d 128), batch 32, ctx 1024-4096, "
+                      "32-node depth-6 trees",
+            "gpu_us": us, "algorithmic_bytes": nbytes, "GBs": gbs, "frac": gbs / HBM_PEAK_GBS,
+            "cpu_oracle_us": cus * B / ns, "sample": f"{ns} of {B} sequences, scaled",
+            "parity_with_oracle": err <= 2e-2, "max_abs_err": err,
+            "note": f"max abs error vs oracle on the sample {err:.2e} (tolerance 2e-2)"}
 
 
 def run_kernels(args):
@@ -450,17 +589,7 @@ def run_kernels(args):
     V = 151936
 
     def gpu_us(fn, timer, iters=20, warm=3):
-        for _ in range(warm):
-            fn()
-        torch.cuda.synchronize()
-        _C.timing_reset()
-        _C.timing_enable(True)
-        for _ in range(iters):
-            fn()
-        torch.cuda.synchronize()
-        _C.timing_enable(False)
-        ms, n = _C.timing_read(timer)
-        return ms / n * 1e3
+        return gpu_launch_us(torch, fn, timer, iters, warm)
 
     def cpu_us(fn, reps=1):
         t0 = time.perf_counter()
@@ -523,30 +652,9 @@ def run_kernels(args):
 
     # -- tree attention, Qwen3-0.6B shape: batch 32, ctx 1024-4096, 32-node depth-6 trees
     log("tree attention (0.6B shape)")
-    B, T, Hq, Hkv, D = 32, 32, 16, 8, 128
-    rng = np.random.default_rng(args.seed + 2)
-    vb = VerifyBatch.random(B, (1024, 4096), T, 6, 256, rng)
-    g = torch.Generator().manual_seed(args.seed + 2)
-    kc = (torch.randn(vb.num_blocks, 256, Hkv, D, generator=g)).to(torch.bfloat16)
-    vc = (torch.randn(vb.num_blocks, 256, Hkv, D, generator=g)).to(torch.bfloat16)
-    N = int(vb.cu_q[-1])
-    q = torch.randn(N, Hq, D, generator=g).to(torch.bfloat16)
-    t = lambda a, dt=torch.int32: torch.from_numpy(a).to(dev, dt)
-    qd, kcd, vcd = q.to(dev), kc.to(dev), vc.to(dev)
-    a_args = (qd, kcd, vcd, t(vb.bt), t(vb.cu_q), t(vb.context_lens), D ** -0.5,
-              t(vb.masks, torch.int64), T, int(vb.context_lens.max()))
-    us = gpu_us(lambda: tree_attention(*a_args), _C.TIMER_TREE_ATTENTION)
-    o = tree_attention(*a_args).float().cpu().numpy()
-    ns = 4
-    rows = int(vb.cu_q[ns])
-    cus, ref = cpu_us(lambda: oatt.paged_attention(
-        q[:rows].float().numpy(), kc.float().numpy(), vc.float().numpy(), vb.bt[:ns],
-        vb.cu_q[:ns + 1], vb.context_lens[:ns], vb.masks[:rows].view(np.uint64), D ** -0.5, 256))
-    err = float(np.abs(o[:rows] - ref).max())
-    nbytes = float(vb.context_lens.sum()) * Hkv * D * 2 * 2 + 2.0 * N * Hq * D * 2
-    emit("tree_attention", "Qwen3-0.6B shape (16/8 heads, d 128), batch 32, ctx 1024-4096, "
-         "32-node depth-6 trees", us, nbytes, cus * B / ns, f"{ns} of {B} sequences, scaled",
-         err <= 2e-2, f"max abs error vs oracle on the sample {err:.2e} (tolerance 2e-2)")
+    c3 = attention_small_tree(torch, dev, args.seed, gpu_us, check_seqs=4)
+    emit("tree_attention", c3["config"], c3["gpu_us"], c3["algorithmic_bytes"],
+         c3["cpu_oracle_us"], c3["sample"], c3["parity_with_oracle"], c3["note"])
 
     # -- causal paged prefill (the attention kernel with no tree mask), Qwen3-8B heads:
     #    4 prompts of 2048 tokens whose K/V are already in the cache
@@ -799,6 +907,16 @@ def main():
                     "GBs": sampler_gbs, "frac": sampler_gbs / HBM_PEAK_GBS},
         "kernels_us_per_step": {k: v[0] / args.steps * 1e3 for k, v in timers.items()},
     }
+    if args.small_tree_attention:
+        # tree attention at the Qwen3-0.6B shape (32 ragged sequences, 32-node trees),
+        # timed after the verify steps, with a parity check on a sample
+        print("[bench] tree attention, Qwen3-0.6B shape", file=sys.stderr, flush=True)
+        c3 = attention_small_tree(torch, dev, args.seed, lambda fn, timer: gpu_launch_us(
+            torch, fn, timer), check_seqs=2)
+        out["tree_attention_0p6b"] = {k: c3[k] for k in (
+            "config", "gpu_us", "algorithmic_bytes", "GBs", "frac", "parity_with_oracle",
+            "max_abs_err", "sample")}
+        out["tree_attention_0p6b"]["sample"] = "parity: first 2 of 32 sequences vs the oracle"
     if args.calib_copy:
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)

@@ -172,12 +172,20 @@ int nvx_temperature_softmax(const void* logits, int32_t logits_dtype, int64_t lo
  * -1 padded), accepted_len int32 [num_seqs] (accepted draft nodes), out_tokens
  * int32 [num_seqs, node_stride] (accepted tokens then the next token, -1 padded),
  * next_token int32 [num_seqs].  Limits: 1 <= node_stride <= 64, vocab <= 2,097,152.
- * Up to 256 sequences are walked by 16, 8, 4 or 2 workgroups each (the most for
- * which the whole grid fits on the GPU at once), which meet through a static
- * per-GPU array: calls that overlap on one GPU (two streams) race, so serialise
- * them (or bound the width to 1, below).  If a sequence's workgroups fail to meet
+ *
+ * Workspace (caller-owned, device memory): with a workspace of at least
+ * nvx_rejection_walk_workspace_size(num_seqs) bytes (8-byte aligned), each sequence
+ * is walked by 16, 8, 4 or 2 workgroups (the most for which the whole grid fits on
+ * the GPU at once; 1 under stream capture), which meet through exchange slots in
+ * the workspace.  It must be zero-filled before its first use and is then kept by
+ * the library from call to call (it holds each sequence's exchange counter), so do
+ * not reuse it for anything else.  Walks that overlap in time (different streams)
+ * need different workspaces, and together must fit on the GPU at once.  With
+ * workspace = NULL each sequence is walked by one workgroup and no state is shared:
+ * any number of such calls may overlap.  If a sequence's workgroups fail to meet
  * within about a second (a device shared with a kernel that never ends), its
- * outputs are all -1.  Outputs do not depend on the width.
+ * outputs are all -1 (accepted_len = next_token = -1): callers must check
+ * accepted_len >= 0.  Outputs do not depend on the number of workgroups.
  */
 int nvx_rejection_sample_tree(const float* target_probs, int64_t p_seq_stride,
                               const float* draft_probs, int64_t q_seq_stride, int32_t vocab,
@@ -186,14 +194,22 @@ int nvx_rejection_sample_tree(const float* target_probs, int64_t p_seq_stride,
                               const float* uniforms, const float* final_uniforms,
                               const uint8_t* greedy, int32_t draft_mode, int32_t num_seqs,
                               int32_t* path, int32_t* accepted_len, int32_t* out_tokens,
-                              int32_t* next_token, void* stream);
+                              int32_t* next_token, void* workspace, size_t workspace_bytes,
+                              void* stream);
+
+/* nvx_rejection_walk_workspace_size: no counterpart in the reference.  Bytes of the
+ * exchange workspace a tree / chain rejection walk of num_seqs sequences needs
+ * (1,280 per sequence; 0 for num_seqs <= 0).  Sequence b always uses the same
+ * 1,280 bytes, so one workspace serves walks of any batch size up to the one it was
+ * sized for.
+ */
+size_t nvx_rejection_walk_workspace_size(int32_t num_seqs);
 
 /* nvx_rejection_walk_max_width: no counterpart in the reference.  Bounds the
  * workgroups per sequence of later tree / chain rejection walks in this process
  * (1, 2, 4, 8 or 16; other values in [1, 16] round down to one of those) and returns
  * the previous bound, or -1 for a value outside [1, 16].  Width 1 needs no
- * cross-workgroup exchange, so walks that run concurrently on several streams are
- * safe under it.  The default is 16.
+ * cross-workgroup exchange (as a NULL workspace).  The default is 16.
  */
 int nvx_rejection_walk_max_width(int32_t max_width);
 
@@ -234,7 +250,8 @@ int nvx_rejection_sample_tree_logits(const void* logits, int32_t logits_dtype,
                                      const float* final_uniforms, const uint8_t* greedy,
                                      int32_t draft_mode, int32_t num_seqs, int32_t* path,
                                      int32_t* accepted_len, int32_t* out_tokens,
-                                     int32_t* next_token, void* stream);
+                                     int32_t* next_token, void* workspace,
+                                     size_t workspace_bytes, void* stream);
 
 /* -------------------------------------------------- fused model layers --
  * Elementwise layers of the target model around the verify-path attention, each

@@ -484,7 +484,6 @@ __device__ __forceinline__ void residual8(const PRow& prow, const float* qrow, i
 // and picks are the same bits for every K.
 constexpr int kLW = 64;
 constexpr int kMaxVocab = kSub * 64 * kLW;   // R <= 64: a lane can hold a subtile index
-constexpr int kMaxCoopSeqs = 256;            // sequences of a multi-workgroup walk
 constexpr int kSlots = 2 * kLW;              // per sequence: two banks of 64 exchange slots
 constexpr uint32_t kMaxSpins = 1u << 20;     // bound on a wait for an exchanged value
 constexpr uint32_t kFailSkip = 1024;         // > the exchanges of one walk (2 * kMaxNodes + 3)
@@ -504,16 +503,25 @@ struct Layout {
   __device__ __forceinline__ int hi(int lw) const { return min(lw * R + R, nsub); }
 };
 
-// The walk's cross-workgroup state, in static device arrays (zero when the library
-// loads).  Per sequence: kSlots 64-bit exchange slots, each holding (exchange number
-// << 32) | value, so a value and the exchange it belongs to are read in one atomic
-// load and no fence or counter orders them; two banks alternate by exchange, so a
-// slot is not rewritten while another workgroup may still wait on it.  walk_base
-// holds, per sequence, the last exchange number used: a walk numbers its exchanges
-// from there, so slots left by earlier walks never match (a walk that timed out
-// moves the base past every number it may have used).
-__device__ __align__(256) uint64_t walk_slots[kMaxCoopSeqs * kSlots];
-__device__ __align__(256) uint32_t walk_base[kMaxCoopSeqs];
+// The walk's cross-workgroup state lives in the caller's workspace (zero-filled
+// before its first use, then kept by the library), one fixed-size record per
+// sequence index at b * kRecWords 64-bit words, so walks of any batch size that
+// reuse one workspace see the same record for sequence b:
+//  * kSlots 64-bit exchange slots, each holding (exchange number << 32) | value, so a
+//    value and the exchange it belongs to are read in one atomic load and no fence
+//    or counter orders them; two banks alternate by exchange, so a slot is not
+//    rewritten while another workgroup may still wait on it;
+//  * then one uint32, the last exchange number used: a walk numbers its exchanges
+//    from there, so slots left by earlier walks never match (a walk that timed out
+//    moves the base past every number it may have used).
+// slots (two 512-byte banks), then the base in a 256-byte tail: a record is 1,280 bytes,
+// so every bank starts on a 256-byte boundary and no cache line holds two sequences'
+// slots
+constexpr int kRecWords = kSlots + 32;
+inline size_t walk_workspace_bytes(int num_seqs) {
+  const size_t n = num_seqs > 0 ? (size_t)num_seqs : 0;
+  return (n * kRecWords * sizeof(uint64_t) + 255) & ~(size_t)255;
+}
 
 struct Coop {
   uint64_t* slots;  // this sequence's slots (K > 1)
@@ -859,6 +867,7 @@ struct WalkArgs {
   int32_t* tok_out;
   int32_t* next_out;
   bool vp, vq;
+  uint64_t* ex;  // exchange records [num_seqs, kRecWords] (multi-workgroup walks)
 };
 
 __device__ void write_walk(const WalkArgs& a, int b, bool failed, int depth, int next,
@@ -896,7 +905,8 @@ void rejection_walk_kernel(Src src, WalkArgs a) {
 
   const int lane = threadIdx.x & 63;
   const int b = blockIdx.x / K;
-  Coop co{K > 1 ? walk_slots + (size_t)b * kSlots : nullptr, K > 1 ? walk_base + b : nullptr, K,
+  uint64_t* const rec = K > 1 ? a.ex + (size_t)b * kRecWords : nullptr;
+  Coop co{rec, K > 1 ? reinterpret_cast<uint32_t*>(rec + kSlots) : nullptr, K,
           (int)(blockIdx.x % K), 0u, &s_flag};
   if (K > 1) co.n = __hip_atomic_load(co.base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int V = a.V;
@@ -1077,7 +1087,8 @@ std::atomic<int> g_walk_max_width{kMaxWidth};
 
 // Workgroups per sequence for a walk of num_seqs sequences: the largest of 16, 8, 4
 // and 2 (at most the set bound) for which all the walk's workgroups fit on the device
-// at once, when the stream is not being captured; else 1.  More workgroups per
+// at once, when the caller gave an exchange workspace and the stream is not being
+// captured; else 1.  More workgroups per
 // sequence spread one sequence's row passes over more CUs (same total waves), which
 // shortens the passes of the sequences that are still walking when the others are
 // done.  The K workgroups of a sequence wait for each other, so they must all be
@@ -1086,8 +1097,8 @@ std::atomic<int> g_walk_max_width{kMaxWidth};
 // workgroups still fail to meet (a device shared with a kernel that never ends),
 // the bounded waits end the walk with the failure outputs rather than a hang.
 template <typename Src>
-int walk_width(int num_seqs, hipStream_t s) {
-  if (num_seqs > kMaxCoopSeqs) return 1;
+int walk_width(int num_seqs, hipStream_t s, bool have_workspace) {
+  if (!have_workspace) return 1;
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
     (void)hipGetLastError();
@@ -1111,7 +1122,7 @@ hipError_t launch_walk(const Src& src, const WalkArgs& a, int num_seqs, hipStrea
 #define NVX_WALK(K)                                                                          \
   hipLaunchKernelGGL((rejection_walk_kernel<Src, K>), dim3(num_seqs * K), dim3(walk_nw(K) * 64), 0, \
                      s, src, a)
-  switch (walk_width<Src>(num_seqs, s)) {
+  switch (walk_width<Src>(num_seqs, s, a.ex != nullptr)) {
     case 16: NVX_WALK(16); break;
     case 8: NVX_WALK(8); break;
     case 4: NVX_WALK(4); break;
@@ -1125,6 +1136,26 @@ hipError_t launch_walk(const Src& src, const WalkArgs& a, int num_seqs, hipStrea
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // The row statistics are read and written as float2 (max, 1/sum) pairs.
 inline bool aligned8(const void* p) { return ((uintptr_t)p & 7) == 0; }
+
+// The exchange records of a walk in the caller's workspace: NULL means no exchange
+// (one workgroup per sequence); otherwise it must hold walk_workspace_bytes(num_seqs)
+// and be 8-byte aligned.  Reports a bad workspace and returns false.
+bool walk_exchange(const char* who, void* ws, size_t bytes, int num_seqs, uint64_t** ex) {
+  *ex = nullptr;
+  if (!ws) return true;
+  const size_t need = walk_workspace_bytes(num_seqs);
+  if (bytes < need) {
+    nvx::fail(NVX_EINVAL, "%s: exchange workspace of %zu bytes required for %d sequences (got %zu)",
+              who, need, num_seqs, bytes);
+    return false;
+  }
+  if (!aligned8(ws)) {
+    nvx::fail(NVX_EINVAL, "%s: the exchange workspace must be 8-byte aligned", who);
+    return false;
+  }
+  *ex = static_cast<uint64_t*>(ws);
+  return true;
+}
 
 }  // namespace
 
@@ -1165,6 +1196,10 @@ extern "C" int nvx_temperature_softmax(const void* logits, int32_t logits_dtype,
   return NVX_OK;
 }
 
+extern "C" size_t nvx_rejection_walk_workspace_size(int32_t num_seqs) {
+  return walk_workspace_bytes(num_seqs);
+}
+
 extern "C" int nvx_rejection_walk_max_width(int32_t max_width) {
   nvx::clear_error();
   NVX_CHECK(max_width >= 1 && max_width <= kMaxWidth,
@@ -1181,7 +1216,8 @@ extern "C" int nvx_rejection_sample_tree(const float* target_probs, int64_t p_se
                                          const float* uniforms, const float* final_uniforms,
                                          const uint8_t* greedy, int32_t draft_mode, int32_t num_seqs,
                                          int32_t* path, int32_t* accepted_len, int32_t* out_tokens,
-                                         int32_t* next_token, void* stream) {
+                                         int32_t* next_token, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
   nvx::clear_error();
   NVX_CHECK(num_seqs >= 0 && vocab >= 1, "rejection_sample_tree: bad sizes (seqs=%d, vocab=%d)",
             num_seqs, vocab);
@@ -1195,6 +1231,9 @@ extern "C" int nvx_rejection_sample_tree(const float* target_probs, int64_t p_se
                 accepted_len && out_tokens && next_token,
             "rejection_sample_tree: null pointer");
   NVX_CHECK(vocab <= kMaxVocab, "rejection_sample_tree: vocab %d exceeds %d", vocab, kMaxVocab);
+  uint64_t* ex = nullptr;
+  if (!walk_exchange("rejection_sample_tree", workspace, workspace_bytes, num_seqs, &ex))
+    return NVX_EINVAL;
   hipStream_t s = (hipStream_t)stream;
   nvx::TimerScope timer(NVX_TIMER_REJECTION, s);
   const bool vp = vocab % 4 == 0 && p_seq_stride % 4 == 0 && aligned16(target_probs);
@@ -1202,7 +1241,7 @@ extern "C" int nvx_rejection_sample_tree(const float* target_probs, int64_t p_se
                   (vocab % 4 == 0 && q_seq_stride % 4 == 0 && aligned16(draft_probs));
   const WalkArgs wa{draft_mode == 1 ? nullptr : draft_probs, q_seq_stride, vocab, tokens, parents,
                     num_nodes, node_stride, uniforms, final_uniforms, greedy, draft_mode, path,
-                    accepted_len, out_tokens, next_token, vp, vq};
+                    accepted_len, out_tokens, next_token, vp, vq, ex};
   NVX_HIP(launch_walk(ProbSource{target_probs, p_seq_stride, vocab}, wa, num_seqs, s));
   return NVX_OK;
 }
@@ -1277,7 +1316,8 @@ extern "C" int nvx_rejection_sample_tree_logits(
     int32_t vocab, const int32_t* tokens, const int32_t* parents, const int32_t* num_nodes,
     int32_t node_stride, const float* uniforms, const float* final_uniforms, const uint8_t* greedy,
     int32_t draft_mode, int32_t num_seqs, int32_t* path, int32_t* accepted_len,
-    int32_t* out_tokens, int32_t* next_token, void* stream) {
+    int32_t* out_tokens, int32_t* next_token, void* workspace, size_t workspace_bytes,
+    void* stream) {
   nvx::clear_error();
   NVX_CHECK(logits_dtype == NVX_DTYPE_F32 || logits_dtype == NVX_DTYPE_BF16,
             "rejection_sample_tree_logits: logits must be fp32 or bf16 (dtype code %d)",
@@ -1299,6 +1339,9 @@ extern "C" int nvx_rejection_sample_tree_logits(
   NVX_CHECK(aligned8(stats), "rejection_sample_tree_logits: stats must be 8-byte aligned");
   NVX_CHECK(vocab <= kMaxVocab, "rejection_sample_tree_logits: vocab %d exceeds %d", vocab,
             kMaxVocab);
+  uint64_t* ex = nullptr;
+  if (!walk_exchange("rejection_sample_tree_logits", workspace, workspace_bytes, num_seqs, &ex))
+    return NVX_EINVAL;
   hipStream_t s = (hipStream_t)stream;
   nvx::TimerScope timer(NVX_TIMER_REJECTION, s);
   const bool bf16 = logits_dtype == NVX_DTYPE_BF16;
@@ -1309,7 +1352,7 @@ extern "C" int nvx_rejection_sample_tree_logits(
   const float2* st = reinterpret_cast<const float2*>(stats);
   const WalkArgs wa{draft_mode == 1 ? nullptr : draft_probs, q_seq_stride, vocab, tokens, parents,
                     num_nodes, node_stride, uniforms, final_uniforms, greedy, draft_mode, path,
-                    accepted_len, out_tokens, next_token, vp, vq};
+                    accepted_len, out_tokens, next_token, vp, vq, ex};
   if (bf16)
     NVX_HIP(launch_walk(LogitSource<uint16_t>{(const uint16_t*)logits, logits_row_stride,
                                               node_stride, temperatures, st},

@@ -41,7 +41,8 @@ _SIGS = {
     "nvx_rejection_sample_tree": ([c_void_p, c_int64, c_void_p, c_int64, c_int32, c_void_p,
                                    c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p,
                                    c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p,
-                                   c_void_p], c_int32),
+                                   c_void_p, c_size_t, c_void_p], c_int32),
+    "nvx_rejection_walk_workspace_size": ([c_int32], c_size_t),
     "nvx_rmsnorm": ([c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
                      c_float, c_void_p], c_int32),
     "nvx_qk_norm_rope": ([c_void_p, c_int64, c_int32, c_int32, c_int32, c_void_p, c_void_p,
@@ -55,7 +56,8 @@ _SIGS = {
     "nvx_rejection_sample_tree_logits": ([c_void_p, c_int32, c_int64, c_void_p, c_void_p, c_void_p,
                                           c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_int32,
                                           c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p,
-                                          c_void_p, c_void_p, c_void_p, c_void_p], c_int32),
+                                          c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
+                                          c_void_p], c_int32),
     "nvx_topk_logprobs": ([c_void_p, c_int32, c_int64, c_int32, c_int32, c_int32, c_void_p,
                            c_void_p, c_void_p], c_int32),
     "nvx_rejection_walk_max_width": ([c_int32], c_int32),

@@ -63,9 +63,15 @@ class LLMEngine:
             if self.tokenizer is None:
                 raise ValueError("text prompts need a tokenizer in the model directory")
             prompt = self.tokenizer.encode(prompt)
-        # every position a step writes (prompt, completion, draft rows) must have a
-        # RoPE table entry
-        span = len(prompt) + sampling_params.max_tokens + self.config.verify_lookahead
+        # The engine is sized for max_model_len tokens per sequence (the graphs' block
+        # tables, the n-gram history buffers), and every position a step writes
+        # (prompt, completion, draft rows) must have a RoPE table entry.
+        length = len(prompt) + sampling_params.max_tokens
+        if length > self.config.max_model_len:
+            raise ValueError(f"prompt of {len(prompt)} tokens + max_tokens "
+                             f"{sampling_params.max_tokens} exceeds max_model_len "
+                             f"{self.config.max_model_len}")
+        span = length + self.config.verify_lookahead
         if span > self._max_positions:
             raise ValueError(f"prompt of {len(prompt)} tokens + max_tokens "
                              f"{sampling_params.max_tokens} + {self.config.verify_lookahead} "

@@ -1,8 +1,10 @@
 """ModelRunner: one process driving one GPU.
 
 Follows the reference's runner (nanovllm/engine/model_runner.py:15-220): paged KV
-allocation, host-side packing of the batch, the model forward and sampling.  Tensor
-parallel workers, the shm RPC and CUDA-graph capture are left out.
+allocation, host-side packing of the batch, the model forward and sampling, and
+HIP-graph capture of the decode / verify steps (model_runner.py:222-257; on by
+default, as there).  Tensor-parallel workers and the shm RPC are left out: the path
+runs on one GPU.
 
 Speculative decoding (``speculative_method="ngram"``) replaces the decode step by
 a verify step:
@@ -306,8 +308,8 @@ class ModelRunner:
     # (context 0, slot -1: nothing stored, output rows 0).  The LM head and the
     # sampler run outside the graph.  With EAGLE-3 the graph is the target's tree
     # verify (T = tree nodes) and also returns the aux residual streams the draft head
-    # fuses; the draft tree expansion is captured per batch size too, and the
-    # draft catch-up runs eagerly.
+    # fuses; the draft tree expansion and the draft catch-up are captured per batch
+    # size too.
 
     def _graph_rows(self):
         """Rows per sequence of the captured graphs: the EAGLE-3 tree, or both a plain
@@ -503,7 +505,7 @@ class ModelRunner:
             input_ids, positions = self.prepare_prefill(seqs)
             temperatures = self.prepare_sample(seqs)
             logits = self.run_model(input_ids, positions, True)
-            token_ids = self.sampler(logits, temperatures).tolist()
+            token_ids = self._sampled(self.sampler(logits, temperatures).tolist())
             reset_context()
             return token_ids
         drafts = (self.proposer.propose_seqs([seq.seq_id for seq in seqs],
@@ -515,16 +517,43 @@ class ModelRunner:
         reset_context()
         B = len(seqs)
         if T == 1:
-            return [[t] for t in self.sampler(logits, temperatures).tolist()]
+            return [[t] for t in self._sampled(self.sampler(logits, temperatures).tolist())]
         tokens = input_ids.view(B, T).to(torch.int32)
         parents = self._chain(T)[0].repeat(B, 1)
-        U = torch.rand(B, T, device="cuda", generator=self.gen)
-        Uf = torch.rand(B, device="cuda", generator=self.gen)
+        U, Uf = self._uniforms(B, T)
         _, acc, out_tokens, _ = self.rejection(logits, temperatures, None, tokens, parents, U, Uf,
                                                num_nodes)
-        acc, out_tokens = acc.tolist(), out_tokens.tolist()
+        return self._verified_tokens(acc.tolist(), out_tokens.tolist())
+
+    def _uniforms(self, B, T):
+        """The walk's uniforms: [B, T] for the acceptance tests, [B] for the final draws."""
+        dev = self.gen.device
+        return (torch.rand(B, T, device=dev, generator=self.gen),
+                torch.rand(B, device=dev, generator=self.gen))
+
+    @staticmethod
+    def _sampled(token_ids):
+        """Host list of the sampler's tokens; a -1 (a walk whose workgroups failed to
+        meet) is refused before it can reach the scheduler or an embedding lookup."""
+        if token_ids and min(token_ids) < 0:
+            bad = [i for i, t in enumerate(token_ids) if t < 0]
+            raise RuntimeError(f"sampler walk failed for {len(bad)} of {len(token_ids)} rows "
+                               f"(rows {bad[:8]}{' ...' if len(bad) > 8 else ''})")
+        return token_ids
+
+    def _verified_tokens(self, acc, out_tokens):
+        """Host lists of the walk's outputs -> each sequence's accepted tokens followed by
+        its recovered / bonus token.  A multi-workgroup walk whose workgroups failed to
+        meet writes accepted_len = -1 (and -1 tokens); such a step is refused here, before
+        anything is counted, handed to the scheduler or used as a draft root."""
+        bad = [b for b, a in enumerate(acc) if a < 0]
+        if bad:
+            raise RuntimeError(
+                f"tree rejection walk failed for {len(bad)} of {len(acc)} sequences (batch rows "
+                f"{bad[:8]}{' ...' if len(bad) > 8 else ''}): its workgroups did not meet within "
+                f"the bounded wait, so this verify step produced no tokens")
         self._count(acc)
-        return [out_tokens[b][:acc[b] + 1] for b in range(B)]
+        return [out_tokens[b][:acc[b] + 1] for b in range(len(acc))]
 
     def _count(self, acc):
         st = self.spec_stats
@@ -570,7 +599,8 @@ class ModelRunner:
         hidden, aux = self.model(input_ids, positions, self.draft.aux_layers)
         cu = get_context().cu_seqlens_q
         last = cu[1:].long() - 1
-        token_ids = self.sampler(self.model.compute_logits(hidden[last]), temperatures).tolist()
+        token_ids = self._sampled(
+            self.sampler(self.model.compute_logits(hidden[last]), temperatures).tolist())
         # Draft catch-up on the chunk: row q takes token q+1 (the sampled token after
         # the prompt's last position) and the target feature at q.  Same attention
         # context as the target's prefill (positions, slots, block tables).
@@ -678,15 +708,15 @@ class ModelRunner:
         logits = self.model.compute_logits(hidden)
         reset_context()
         temperatures = self.prepare_sample(seqs)
-        U = torch.rand(B, T, device="cuda", generator=self.gen)
-        Uf = torch.rand(B, device="cuda", generator=self.gen)
+        U, Uf = self._uniforms(B, T)
         tok32, par32 = tokens.to(torch.int32), parents.to(torch.int32)
         path, acc, out_tokens, _ = self.rejection(logits, temperatures, None, tok32, par32, U, Uf)
         ctx32 = ctx_d.to(torch.int32)
+        # a failed walk row (accepted_len -1) compacts nothing; the check after the
+        # read-back raises before the catch-up could take another row as its root
         kv_compact(self.kv_cache[0], self.kv_cache[1], block_tables, ctx32, path, acc)
-        acc_h, out_h = acc.tolist(), out_tokens.tolist()
-        self._count(acc_h)
-        result = [out_h[b][:acc_h[b] + 1] for b in range(B)]
+        acc_h = acc.tolist()
+        result = self._verified_tokens(acc_h, out_tokens.tolist())
         # Draft catch-up: rows ctx .. ctx+a take the accepted tokens then the bonus /
         # recovered token, with the target features of the accepted path's tree rows.
         # After the read-back, so the GPU runs it while the host schedules the next step.

@@ -108,6 +108,11 @@ class Scheduler:
         bm = self.block_manager
         for seq, new in zip(seqs, token_ids):
             new = [new] if isinstance(new, int) else list(new)
+            if not is_prefill and (not new or min(new) < 0):
+                # a step always yields at least the recovered / bonus token; -1 marks a
+                # failed walk row, never a token
+                raise RuntimeError(f"sequence {seq.seq_id}: a decode step must append at least "
+                                   f"one token id >= 0 (got {new})")
             if is_prefill:
                 cached = seq.num_cached_tokens + seq.num_scheduled_tokens
                 bm.hash_blocks(seq, cached)

@@ -61,8 +61,34 @@ def _i32(t):
     return t.to(torch.int32).contiguous()
 
 
+_WALK_WS = {}  # (device index, stream) -> zero-filled uint8 tensor, grown on demand
+
+
+def walk_workspace(num_seqs, device, workspace=None):
+    """(tensor, bytes) of the exchange workspace for a walk of num_seqs sequences on the
+    current stream of `device`.  The walk spreads each sequence over several
+    workgroups, which meet through this memory; it must be zero-filled before its first
+    use and is then owned by the library (it keeps per-sequence exchange counters).
+    One workspace per (device, stream): walks on one stream run in order, and walks on
+    different streams never share one.  A workspace passed in is used as given (the
+    caller zero-fills it once and keeps it for walks that never overlap).  Under stream
+    capture the walk runs one workgroup per sequence and takes none."""
+    if workspace is not None:
+        return workspace, workspace.numel() * workspace.element_size()
+    if torch.cuda.is_current_stream_capturing():
+        return None, 0
+    need = _C.lib().nvx_rejection_walk_workspace_size(num_seqs)
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _WALK_WS.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(max(need, _C.lib().nvx_rejection_walk_workspace_size(256)),
+                         dtype=torch.uint8, device=device)
+        _WALK_WS[key] = ws
+    return ws, ws.numel()
+
+
 def rejection_sample_tree(target_probs, draft_probs, tokens, parents, uniforms, final_uniforms,
-                          greedy=None, num_nodes=None, draft_mode="stochastic"):
+                          greedy=None, num_nodes=None, draft_mode="stochastic", workspace=None):
     """Verify one draft tree per sequence.
 
     target_probs fp32 [B, T, V] (row i: target distribution after node i);
@@ -70,9 +96,11 @@ def rejection_sample_tree(target_probs, draft_probs, tokens, parents, uniforms, 
     T' >= number of internal-node rows used) or None with draft_mode="delta";
     tokens, parents int [B, T] (parents[:, 0] = -1, parents[b, i] < i);
     uniforms fp32 [B, T]; final_uniforms fp32 [B]; greedy bool [B] or None;
-    num_nodes int [B] or None (ragged trees).
+    num_nodes int [B] or None (ragged trees); workspace: the walk's exchange memory
+    (see walk_workspace; by default one kept per device and stream).
 
     Returns int32 (path [B, T], accepted_len [B], out_tokens [B, T], next_token [B]).
+    accepted_len is -1 for a sequence whose workgroups failed to meet (callers check).
     """
     B, T, V = target_probs.shape
     if target_probs.dtype != torch.float32 or target_probs.stride(2) != 1 \
@@ -96,12 +124,15 @@ def rejection_sample_tree(target_probs, draft_probs, tokens, parents, uniforms, 
     acc = torch.empty(B, dtype=torch.int32, device=dev)
     out_tokens = torch.empty(B, T, dtype=torch.int32, device=dev)
     nxt = torch.empty(B, dtype=torch.int32, device=dev)
-    _C.require_cuda(target_probs, draft_probs, tokens, parents, uniforms, final_uniforms, g, nn_)
+    _C.require_cuda(target_probs, draft_probs, tokens, parents, uniforms, final_uniforms, g, nn_,
+                    workspace)
+    ws, ws_bytes = walk_workspace(B, dev, workspace)
     _C.check(_C.lib().nvx_rejection_sample_tree(
         _C.ptr(target_probs), target_probs.stride(0), None if delta else _C.ptr(draft_probs),
         0 if delta else draft_probs.stride(0), V, _C.ptr(tokens), _C.ptr(parents), _C.ptr(nn_), T,
         _C.ptr(uniforms), _C.ptr(final_uniforms), _C.ptr(g), 1 if delta else 0, B, _C.ptr(path),
-        _C.ptr(acc), _C.ptr(out_tokens), _C.ptr(nxt), _C.stream_of(target_probs)))
+        _C.ptr(acc), _C.ptr(out_tokens), _C.ptr(nxt), _C.ptr(ws), ws_bytes,
+        _C.stream_of(target_probs)))
     return path, acc, out_tokens, nxt
 
 
@@ -156,7 +187,7 @@ def softmax_from_stats(logits: torch.Tensor, temperatures: torch.Tensor, stats: 
 
 def rejection_sample_tree_logits(logits, temperatures, stats, draft_probs, tokens, parents,
                                  uniforms, final_uniforms, greedy=None, num_nodes=None,
-                                 draft_mode="stochastic"):
+                                 draft_mode="stochastic", workspace=None):
     """rejection_sample_tree with the target rows given as logits [B*T, V] (row b*T + i
     for node i of sequence b), their temperatures [B*T] and softmax_stats: each
     probability the walk reads is recomputed from the logits and statistics, so the
@@ -188,13 +219,14 @@ def rejection_sample_tree_logits(logits, temperatures, stats, draft_probs, token
     out_tokens = torch.empty(B, T, dtype=torch.int32, device=dev)
     nxt = torch.empty(B, dtype=torch.int32, device=dev)
     _C.require_cuda(logits, temperatures, stats, draft_probs, tokens, parents, uniforms,
-                    final_uniforms, g, nn_)
+                    final_uniforms, g, nn_, workspace)
+    ws, ws_bytes = walk_workspace(B, dev, workspace)
     _C.check(_C.lib().nvx_rejection_sample_tree_logits(
         _C.ptr(logits), _DTYPE_CODE[logits.dtype], logits.stride(0), _C.ptr(temperatures),
         _C.ptr(stats), None if delta else _C.ptr(draft_probs), 0 if delta else draft_probs.stride(0),
         V, _C.ptr(tokens), _C.ptr(parents), _C.ptr(nn_), T, _C.ptr(uniforms), _C.ptr(final_uniforms),
         _C.ptr(g), 1 if delta else 0, B, _C.ptr(path), _C.ptr(acc), _C.ptr(out_tokens), _C.ptr(nxt),
-        _C.stream_of(logits)))
+        _C.ptr(ws), ws_bytes, _C.stream_of(logits)))
     return path, acc, out_tokens, nxt
 
 

@@ -53,8 +53,9 @@ y, added in order, and the pick is the first y with F(y) > tau and v(y) > 0, els
 the lane's last y with v(y) > 0.  When no lane ends above tau (u * sum rounds to the
 sum) the largest y with v(y) > 0 is picked (-1 for an all-zero row).  Any fixed
 order of the elements gives an exact inverse-CDF sampler; this one needs no
-cross-lane traffic while a row streams, and splits into 1, 2 or 4 workgroups of 16
-waves per sequence without changing a bit.  The pick works on the unnormalised
+cross-lane traffic while a row streams, and splits into 1, 2, 4, 8 or 16 workgroups
+per sequence (16 waves each up to 4 workgroups, then 64 / workgroups; each real wave
+holds 64 / (workgroups x waves) logical waves) without changing a bit.  The pick works on the unnormalised
 residual max(p - c*q, 0) (stochastic) or p with rejected tokens zeroed (delta): the
 kernel picks from the lane sums of the pass that computed the last normaliser.
 

@@ -40,8 +40,16 @@ def test_validation_errors_are_reported():
                                 8, 8, 64, 256, 1.0, None, 0, None)
     assert rc == -1 and b"head_dim" in lib.nvx_last_error()
     rc = lib.nvx_rejection_sample_tree(None, 0, None, 0, 10, None, None, None, 65, None, None, None,
-                                       0, 1, None, None, None, None, None)
+                                       0, 1, None, None, None, None, None, 0, None)
     assert rc == -1 and b"node_stride" in lib.nvx_last_error()
+    # the walk's exchange workspace: 1280 bytes per sequence
+    assert lib.nvx_rejection_walk_workspace_size(0) == 0
+    assert lib.nvx_rejection_walk_workspace_size(1) == 1280
+    assert lib.nvx_rejection_walk_workspace_size(64) == 64 * 1280
+    h = ctypes.c_void_p(0x100000)  # non-null host addresses: refused before any launch
+    rc = lib.nvx_rejection_sample_tree(h, 10, None, 0, 10, h, h, None, 1, h, h, None, 1, 2, h, h, h,
+                                       h, h, 2000, None)
+    assert rc == -1 and b"exchange workspace of 2560 bytes" in lib.nvx_last_error()
     with pytest.raises(RuntimeError, match="kv_compact"):
         _C.check(lib.nvx_kv_compact(None, None, 0, 1, 24, 256, None, 1, None, None, 9, None, 1, None))
     rc = lib.nvx_rejection_walk_max_width(0)
@@ -62,7 +70,7 @@ def test_validation_errors_are_reported():
     assert rc == -1 and b"8-byte aligned" in lib.nvx_last_error()
     rc = lib.nvx_rejection_sample_tree_logits(None, _C.DTYPE_BF16, 64, None, None, None, 0, 64, None,
                                               None, None, 65, None, None, None, 1, 1, None, None,
-                                              None, None, None)
+                                              None, None, None, 0, None)
     assert rc == -1 and b"node_stride" in lib.nvx_last_error()
 
 

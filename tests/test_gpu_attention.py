@@ -134,6 +134,19 @@ def test_config4_tree64_qwen3_8b_layer(dev):
 
 
 @pytest.mark.gpu
+def test_config4_heads_short_context_mask(dev):
+    """Qwen3-8B heads (32/8), 64-node depth-8 trees after only 0-64 cached tokens: the
+    tree keys carry most of the softmax mass, so a wrong mask bit moves outputs by far
+    more than the tolerance (at ctx 2048 the same error would be diluted to ~1e-3).
+    32 sequences, so the 256-row items take the 8-wave workgroup as at config 4."""
+    rng = np.random.default_rng(21)
+    ctx = [int(c) for c in rng.integers(0, 65, size=32)]
+    ctx[:3] = [0, 1, 64]
+    trees = [random_tree(64, 8, rng) for _ in range(32)]
+    run_case(dev, 32, 8, ctx, trees, seed=21)
+
+
+@pytest.mark.gpu
 def test_page_permutation_invariance(dev):
     rng = np.random.default_rng(9)
     g = torch.Generator().manual_seed(9)

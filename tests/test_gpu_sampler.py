@@ -132,9 +132,9 @@ def test_tree_delta_mode(dev):
 @pytest.mark.parametrize("width,B", [(16, 60), (8, 60), (4, 60), (2, 60), (1, 60), (16, 300)])
 def test_walk_widths_are_bit_identical(dev, width, B):
     """Walks bounded to 16, 8, 4, 2 and 1 workgroups per sequence (60 sequences fit the
-    GPU at every width), and 300 sequences (more than a multi-workgroup walk takes, so
-    one workgroup each): every width gives the oracle's outputs, in stochastic, greedy
-    and delta mode."""
+    GPU at every width), and 300 sequences (too many for the grid of a multi-workgroup
+    walk to fit on the GPU at once, so one workgroup each): every width gives the
+    oracle's outputs, in stochastic, greedy and delta mode."""
     lib = _C.lib()
     prev = lib.nvx_rejection_walk_max_width(width)
     try:
@@ -142,6 +142,69 @@ def test_walk_widths_are_bit_identical(dev, width, B):
         tree_case(dev, B=B, T=12, V=3000, depth=4, seed=B + width + 1, delta=True)
     finally:
         assert lib.nvx_rejection_walk_max_width(prev) == width
+
+
+def walk_inputs(B, T, V, depth, seed, greedy_frac=0.25):
+    """Stochastic tree-walk inputs (host tensors) and the oracle's outputs."""
+    rng = np.random.default_rng(seed)
+    g = torch.Generator().manual_seed(seed)
+    P = softmax_rows(g, (B, T, V), 2.0, 0.8)
+    Q = softmax_rows(g, (B, T, V), 2.0, 0.8)
+    parents = np.stack([random_tree(T, depth, rng) for _ in range(B)])
+    Qn = Q.numpy()
+    toks = np.zeros((B, T), np.int32)
+    for b in range(B):
+        for i in range(1, T):
+            row = Qn[b, parents[b, i]].astype(np.float64)
+            toks[b, i] = min(int(np.searchsorted(np.cumsum(row), rng.random() * row.sum())), V - 1)
+    U = rng.random((B, T)).astype(np.float32)
+    Uf = rng.random(B).astype(np.float32)
+    greedy = rng.random(B) < greedy_frac
+    ref = osamp.rejection_sample_tree(P.numpy(), Qn, toks, parents, U, Uf, greedy)
+    args = (P, Q, torch.from_numpy(toks), torch.from_numpy(parents), torch.from_numpy(U),
+            torch.from_numpy(Uf), torch.from_numpy(greedy))
+    return args, ref
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("explicit", [False, True])
+def test_concurrent_walks_on_two_streams(dev, explicit):
+    """Two walks at 16 workgroups per sequence launched on two streams without a
+    synchronisation between them, each with its own exchange workspace (the wrapper's
+    one per stream, or two caller-owned zero-filled ones), twice in a row: all four
+    results equal the oracle bit for bit.  8 sequences per walk, so both grids fit on
+    the GPU together."""
+    from nanovllm.layers.sampler import walk_workspace
+    lib = _C.lib()
+    prev = lib.nvx_rejection_walk_max_width(16)
+    try:
+        cases = [walk_inputs(8, 64, V_QWEN, 8, seed) for seed in (31, 32)]
+        dev_args = [tuple(t.to(dev) for t in a) for a, _ in cases]
+        streams = [torch.cuda.Stream(dev), torch.cuda.Stream(dev)]
+        ws = [None, None]
+        if explicit:
+            n = lib.nvx_rejection_walk_workspace_size(8)
+            ws = [torch.zeros(n, dtype=torch.uint8, device=dev) for _ in range(2)]
+        torch.cuda.synchronize()
+        for rep in range(2):
+            print(f"[walk] two streams explicit={explicit} rep={rep}", flush=True)
+            outs = [None, None]
+            for i in range(2):
+                with torch.cuda.stream(streams[i]):
+                    outs[i] = rejection_sample_tree(*dev_args[i], workspace=ws[i])
+            torch.cuda.synchronize()
+            for i in range(2):
+                for name, a, r in zip(("path", "accepted_len", "out_tokens", "next_token"),
+                                      outs[i], cases[i][1]):
+                    assert np.array_equal(a.cpu().numpy(), r), f"walk {i} rep {rep}: {name} differs"
+        if not explicit:
+            w = []
+            for s in streams:
+                with torch.cuda.stream(s):
+                    w.append(walk_workspace(8, dev)[0])
+            assert w[0].data_ptr() != w[1].data_ptr()
+    finally:
+        assert lib.nvx_rejection_walk_max_width(prev) == 16
 
 
 @pytest.mark.gpu
