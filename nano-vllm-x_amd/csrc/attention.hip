@@ -28,6 +28,7 @@
 // With more than one split, partial (o, log2-sum-exp) go to the workspace and a
 // second kernel merges them.
 #include <mutex>
+#include <type_traits>
 
 #include "nvx_internal.h"
 
@@ -212,15 +213,15 @@ void tree_attn_kernel(AttnParams p) {
   asm volatile("" : : "v"(mbits));
   __syncthreads();
 
-  // Issue the PER LDS-DMA loads of this wave for chunk c into stage st.  Load
-  // j of wave w fills 4 rows (1 KB) of the K (first 16 loads) or V (last 16)
-  // tile; lane i fetches row 4*(ii%16) + i/16, logical segment (i%16)^swz(row),
-  // so the tile lands swizzled.  The per-lane byte offset within a chunk is loop
-  // invariant; the chunk's page start is a scalar base.  In a chunk that ends
-  // past context_len the missing rows re-read the chunk's first row (finite data;
-  // their scores are masked to -inf).
+  // The PER LDS-DMA loads of this wave for one chunk: load j of wave w fills 4 rows
+  // (1 KB) of the K (first 16 loads) or V (last 16) tile; lane i fetches row
+  // 4*(ii%16) + i/16, logical segment (i%16)^swz(row), so the tile lands swizzled.
+  // The per-lane byte offset within a chunk is loop invariant (lane_full, for chunks
+  // wholly before context_len); the chunk's page start is a scalar base.  In the
+  // chunk that ends past context_len the missing rows re-read the chunk's first row
+  // (finite data; their scores are masked to -inf).
   const int row_stride = p.Hkv * kD * 2;  // bytes between consecutive tokens
-  uint32_t lane_off[PER];
+  uint32_t lane_off[PER], lane_full[PER];
   int lane_row[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
@@ -229,47 +230,68 @@ void tree_attn_kernel(AttnParams p) {
     const int seg = (lane & 15) ^ swz(row);
     lane_row[j] = row;
     lane_off[j] = (uint32_t)(hk * kD * 2 + seg * 16);
+    lane_full[j] = lane_off[j] + (uint32_t)(row * row_stride);
   }
-  auto issue_chunk = [&](int c) {
-    const int st = (c - c0) & (kStages - 1);
+  // The chunk to issue next, as (page index in the LDS table, key offset in the page),
+  // advanced by one chunk per issue (no division in the loop).
+  int is_page = 0, is_off = (c0 * kKC) % bs;
+  auto issue_chunk = [&](int c, auto stage) {
+    constexpr int ST = decltype(stage)::value;
     const int pos0 = c * kKC;
-    const int32_t blk = __builtin_amdgcn_readfirstlane(pages[pos0 / bs - page0]);
-    const int64_t tok0 = blk >= 0 ? (int64_t)blk * bs + pos0 % bs : 0;
+    const int32_t blk = __builtin_amdgcn_readfirstlane(pages[is_page]);
+    const int64_t tok0 = blk >= 0 ? (int64_t)blk * bs + is_off : 0;
+    is_off += kKC;
+    if (is_off == bs) {
+      is_off = 0;
+      ++is_page;
+    }
     const char* kbase = reinterpret_cast<const char*>(p.k_cache) + tok0 * row_stride;
     const char* vbase = reinterpret_cast<const char*>(p.v_cache) + tok0 * row_stride;
-    const bool full = pos0 + kKC <= ctxlen;
+    const uint32_t lds0 = ring_base + ST * kStageBytes;
+    if (pos0 + kKC <= ctxlen) {
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int ii = wave + W * j;
-      const int row = full || pos0 + lane_row[j] < ctxlen ? lane_row[j] : 0;
-      dma16<kPolicy>(ii >> 4 ? vbase : kbase, lane_off[j] + (uint32_t)(row * row_stride),
-            ring_base + st * kStageBytes + (ii >> 4) * kTileBytes + (ii & 15) * 1024);
+      for (int j = 0; j < PER; ++j) {
+        const int ii = wave + W * j;
+        dma16<kPolicy>(ii >> 4 ? vbase : kbase, lane_full[j],
+                       lds0 + (ii >> 4) * kTileBytes + (ii & 15) * 1024);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const int ii = wave + W * j;
+        const int row = pos0 + lane_row[j] < ctxlen ? lane_row[j] : 0;
+        dma16<kPolicy>(ii >> 4 ? vbase : kbase, lane_off[j] + (uint32_t)(row * row_stride),
+                       lds0 + (ii >> 4) * kTileBytes + (ii & 15) * 1024);
+      }
     }
   };
 
   // m_run: the row's reference max (scaled log2 units).  The S chain starts from
   // cinit = -m_ref (m_ref = m_run, or 0 before the row's first visible key), so the
-  // MFMAs deliver c*s - m_ref and each probability is one exp2.
+  // MFMAs deliver c*s - m_ref and each probability is one exp2.  Each of the two S
+  // tiles starts from its own copy, so no accumulator is copied per chunk.
   float m_run = -INFINITY, l_run = 0.f;
-  f32x16 cinit;
+  f32x16 cinit[2];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) cinit[j] = 0.f;
+  for (int j = 0; j < 16; ++j) cinit[0][j] = cinit[1][j] = 0.f;
   f32x16 oacc[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int j = 0; j < 16; ++j) oacc[dt][j] = 0.f;
 
-  // LDS byte addresses.  With the swizzle, every read address is a per-lane base
-  // plus the stage offset, XORed with a per-slice constant, plus an immediate:
+  // LDS byte addresses.  With the swizzle, every read address is a per-lane value
+  // (loop invariant, held in registers) plus a constant: the ring stage is a template
+  // constant of each unrolled step, so stage and row offsets become immediates.
   //  K fragment (tile kt, d-slice s): row kt*32 + lr, slot (2s + g) ^ swz(lr)
-  //    = ((stage + k_lane) ^ (s << 5)) + kt * 8192
+  //    = (k_lane ^ (s << 5)) + stage + kt * 8192
   //  V^T transpose read (group ks, d tile dt, half h): 16-lane group q = lane/16
   //  supplies rows (keys) 16*ks + 8*h + 4*(q/2) + i/4 and d columns
   //  dt*32 + 16*(q%2) + 4*(i%4), i.e.
-  //    = ((stage + kTileBytes + v_lane[h]) ^ (dt << 6)) + ks * 4096
+  //    = (v_lane[h] ^ (dt << 6)) + stage + kTileBytes + ks * 4096
   // (swz depends on row % 16 only, so the row terms 32*kt and 16*ks are plain
-  // offsets, and the XORed bits never carry into the row or stage bits.)
+  // offsets, and the XORed bits never carry into the row or stage bits.)  The empty
+  // asm statements keep the compiler from recomputing the XORs in the loop.
   const uint32_t k_lane = (uint32_t)(lr * 256 + ((g ^ swz(lr)) << 4));
   const int tq = lane >> 4, ti = lane & 15;
   const int tr_key = 4 * (tq >> 1) + (ti >> 2);
@@ -277,43 +299,52 @@ void tree_attn_kernel(AttnParams p) {
   const uint32_t v_lane0 = (uint32_t)(tr_key * 256 + ((((tr_d >> 3) ^ swz(tr_key))) << 4) + (tr_d & 7) * 2);
   const uint32_t v_lane1 =
       (uint32_t)((tr_key + 8) * 256 + ((((tr_d >> 3) ^ swz(tr_key + 8))) << 4) + (tr_d & 7) * 2);
+  uint32_t k_addr[8], v_addr[2][4];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    k_addr[s] = k_lane ^ (uint32_t)(s << 5);
+    asm volatile("" : "+v"(k_addr[s]));
+  }
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    v_addr[0][dt] = v_lane0 ^ (uint32_t)(dt << 6);
+    v_addr[1][dt] = v_lane1 ^ (uint32_t)(dt << 6);
+    asm volatile("" : "+v"(v_addr[0][dt]), "+v"(v_addr[1][dt]));
+  }
 
-  // S^T tiles of the chunk in stage st: sacc[kt] element j holds key
+  // S^T tiles of the chunk in stage ST: sacc[kt] element j holds key
   // kt*32 + (j/4)*8 + 4*g + j%4 of query row lr.  s_pair(s) adds the products over
   // d = 16*s .. 16*s+15.
-  auto s_pair = [&](uint32_t kb, int s, f32x16 (&sacc)[2]) {
-    const uint32_t a = kb ^ (uint32_t)(s << 5);
+  auto s_pair = [&](auto stage, int s, f32x16 (&sacc)[2]) {
+    constexpr int ST = decltype(stage)::value;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
-      const bf16x8 k = *reinterpret_cast<const bf16x8*>(ring + a + kt * 8192);
-      sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k, bq[s], s == 0 ? cinit : sacc[kt], 0, 0, 0);
+      const bf16x8 k = *reinterpret_cast<const bf16x8*>(ring + k_addr[s] + ST * kStageBytes + kt * 8192);
+      sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k, bq[s], s == 0 ? cinit[kt] : sacc[kt], 0, 0, 0);
     }
   };
-  // O^T += V^T . P^T for key group ks (keys 16*ks .. 16*ks+15); vb0 / vb1 are the
-  // stage's V tile base plus v_lane0 / v_lane1.
-  auto pv_group = [&](uint32_t vb0, uint32_t vb1, int ks, bf16x8 bp) {
+  // O^T += V^T . P^T for key group ks (keys 16*ks .. 16*ks+15).
+  auto pv_group = [&](auto stage, int ks, bf16x8 bp) {
+    constexpr int ST = decltype(stage)::value;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
-      const uint32_t x = (uint32_t)(dt << 6);
-      const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(ring + ((vb0 ^ x) + ks * 4096)));
-      const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(ring + ((vb1 ^ x) + ks * 4096)));
+      const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+          (lds_bf16x4*)(ring + v_addr[0][dt] + ST * kStageBytes + kTileBytes + ks * 4096));
+      const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+          (lds_bf16x4*)(ring + v_addr[1][dt] + ST * kStageBytes + kTileBytes + ks * 4096));
       const bf16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
       oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bp, oacc[dt], 0, 0, 0);
     }
   };
 
-  // One step on chunk c (in stage st): the S MFMAs into sacc, the softmax (VALU),
+  // One step on chunk c (in stage ST): the S MFMAs into sacc, the softmax (VALU),
   // then the P.V MFMAs.
-  auto step = [&](int c, f32x16 (&sacc)[2]) {
-    const int st = (c - c0) & (kStages - 1);
-    const uint32_t kb = (uint32_t)(st * kStageBytes) + k_lane;
-    const uint32_t vb0 = (uint32_t)(st * kStageBytes + kTileBytes) + v_lane0;
-    const uint32_t vb1 = (uint32_t)(st * kStageBytes + kTileBytes) + v_lane1;
+  auto step = [&](int c, auto stage, f32x16 (&sacc)[2]) {
     if (!wave_active) return;
 
     auto phase_s = [&]() {
 #pragma unroll
-      for (int s = 0; s < 8; ++s) s_pair(kb, s, sacc);
+      for (int s = 0; s < 8; ++s) s_pair(stage, s, sacc);
       // LDS reads run a d-slice ahead of the MFMAs that consume them.
       __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
@@ -325,24 +356,27 @@ void tree_attn_kernel(AttnParams p) {
     };
     // Probabilities of chunk c against the running reference max m_run, packed to
     // bf16 for the P.V MFMAs; returns this lane's fp32 sum of the probabilities.
-    // The sum uses plain fp32 adds: v_dot2 (the bf16 dot product) executes in the
+    // The sum uses plain fp32 adds in two chains (even and odd elements), each
+    // starting from its first term: v_dot2 (the bf16 dot product) executes in the
     // matrix pipe and serialises with the other wave's MFMAs on the SIMD.
     bf16x8 bp[4];
     auto probs = [&]() {
-      float l0 = 0.f, l1 = 0.f;
+      float e[32];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         // P^T as B operand: slot (g, i) of group ks holds key 16*ks + (i/4)*8 +
         // 4*g + i%4, i.e. element (ks&1)*8 + i of sacc[ks/2].
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float e = __builtin_amdgcn_exp2f(sacc[ks >> 1][(ks & 1) * 8 + i]);
-          bp[ks][i] = (__bf16)e;
-          if (i & 1)
-            l1 += e;
-          else
-            l0 += e;
+          e[ks * 8 + i] = __builtin_amdgcn_exp2f(sacc[ks >> 1][(ks & 1) * 8 + i]);
+          bp[ks][i] = (__bf16)e[ks * 8 + i];
         }
+      }
+      float l0 = e[0], l1 = e[1];
+#pragma unroll
+      for (int k = 2; k < 32; k += 2) {
+        l0 += e[k];
+        l1 += e[k + 1];
       }
       return l0 + l1;
     };
@@ -403,7 +437,7 @@ void tree_attn_kernel(AttnParams p) {
 #pragma unroll
           for (int j = 0; j < 16; ++j) sacc[kt][j] += shift;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) cinit[j] = -m_ref_new;
+        for (int j = 0; j < 16; ++j) cinit[0][j] = cinit[1][j] = -m_ref_new;
         lsum = probs();
       }
       l_run += lsum;  // this lane's half of the row; the halves meet at the end
@@ -419,7 +453,7 @@ void tree_attn_kernel(AttnParams p) {
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) pv_group(vb0, vb1, ks, bp[ks]);
+    for (int ks = 0; ks < 4; ++ks) pv_group(stage, ks, bp[ks]);
     // Transpose reads run two MFMAs ahead.
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
@@ -432,14 +466,22 @@ void tree_attn_kernel(AttnParams p) {
   };
 
   // One chunk in flight: wait for chunk c, barrier (every wave is done with chunk
-  // c-1, whose stage receives chunk c+1), then compute chunk c.
+  // c-1, whose stage receives chunk c+1), then compute chunk c.  The loop is unrolled
+  // by the two ring stages, so each step's stage is a compile-time constant.
+  using Stage0 = std::integral_constant<int, 0>;
+  using Stage1 = std::integral_constant<int, 1>;
   f32x16 sacc[2];
-  if (c0 < c1) issue_chunk(c0);
-  for (int c = c0; c < c1; ++c) {
+  if (c0 < c1) issue_chunk(c0, Stage0{});
+  for (int c = c0; c < c1; c += 2) {
     wait_vm<0>();
     __syncthreads();
-    if (c + 1 < c1) issue_chunk(c + 1);
-    step(c, sacc);
+    if (c + 1 < c1) issue_chunk(c + 1, Stage1{});
+    step(c, Stage0{}, sacc);
+    if (c + 1 >= c1) break;
+    wait_vm<0>();
+    __syncthreads();
+    if (c + 2 < c1) issue_chunk(c + 2, Stage0{});
+    step(c + 1, Stage1{}, sacc);
   }
 
   l_run += nvx::shfl_xor_f(l_run, 32);  // both halves share m_run
