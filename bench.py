@@ -3,12 +3,12 @@
 One step = one verify step of 64 sequences, each with 2048 cached context tokens
 and a 64-node depth-8 draft tree: the 36-layer target forward over the 4096 tree
 rows (HIP tree attention over the paged KV cache, torch GEMMs), the LM head, the
-temperature-0.8 sampler (row statistics of the logits, then tree rejection sampling
-against resident fp32 draft probabilities, recomputing the target probabilities of
-the rows it visits), compaction of the accepted paths' KV rows in all 36 layers, and
-the read-back of the accepted lengths.  Weights are random-init bf16 of the
-Qwen3-8B architecture; the cached context K/V, trees, draft distributions and
-tokens are synthetic (seeded).  value = verified tokens/s = sum over the timed
+temperature-0.8 sampler (tree rejection sampling against resident fp32 draft
+probabilities; the walk computes the softmax statistics of the target rows it visits
+and recomputes each probability it reads), compaction of the accepted paths' KV rows
+in all 36 layers, and the read-back of the accepted lengths.  Weights are random-init
+bf16 of the Qwen3-8B architecture; the cached context K/V, trees, draft distributions
+and tokens are synthetic (seeded).  value = verified tokens/s = sum over the timed
 steps of sum_b (accepted_len_b + 1) / elapsed.
 
 Prints one JSON line.  `--gpus N` with N > 1 exits: the verify path runs on a single GPU.
@@ -240,7 +240,9 @@ def build_step(args, torch, dev):
         logits = forward()
         U = torch.rand(B, T, device=dev, generator=ugen)
         Uf = torch.rand(B, device=dev, generator=ugen)
-        path, acc, out_tok, nxt = sampler(logits, temps, Q, tokens32, parents, U, Uf)
+        stats = capture["stats"] if capture is not None else None
+        path, acc, out_tok, nxt = sampler(logits, temps, Q, tokens32, parents, U, Uf,
+                                          stats_out=stats)
         if capture is not None:
             lay, pages = capture["kv_layers"], capture["kv_pages"]
             capture.update(logits=logits, U=U, Uf=Uf, path=path, acc=acc, out_tokens=out_tok,
@@ -412,12 +414,14 @@ def integrated_parity(args, torch, state, step, nseq):
     made greedy with the target's own greedy chain planted on a root-to-leaf path
     (plant_greedy_spines), so the walk accepts deep paths and compaction moves that
     many rows in all layers; the rest stay stochastic at the bench temperature.  The
-    oracle walks the probabilities of the GPU's logits (nvx_softmax_from_stats with
-    the statistics the sampler used, themselves checked against the float64 softmax;
-    the fp32 logits for greedy rows) with the same draft rows, tokens, tree and
-    uniforms, and compacts a copy of the pre-compaction KV pages of the first and last
-    layer along the GPU's paths.  Integer outputs and KV bytes must be equal.  Returns
-    the parity record."""
+    walk computes the statistics of the rows it visits and reports them; the oracle
+    walks the probabilities of the GPU's logits (nvx_softmax_from_stats with those
+    statistics on the visited rows and the statistics pass's elsewhere, all checked
+    against the float64 softmax; the fp32 logits for greedy rows) with the same draft
+    rows, tokens, tree and uniforms, and compacts a copy of the pre-compaction KV pages
+    of the first and last layer along the GPU's paths.  Integer outputs and KV bytes
+    must be equal, and the visited rows must be exactly the sampled sequences' accepted
+    paths.  Returns the parity record."""
     import numpy as np
     from nanovllm.layers.sampler import softmax_from_stats, softmax_stats
     from oracle import kvcache as okv, sampler as osamp
@@ -434,13 +438,17 @@ def integrated_parity(args, torch, state, step, nseq):
                             np.int32)
         layers = [0, L - 1]
         cap = {"kv_layers": torch.tensor(layers, device=dev),
-               "kv_pages": torch.tensor(used, device=dev)}
+               "kv_pages": torch.tensor(used, device=dev),
+               "stats": torch.full((B * T, 2), float("nan"), device=dev)}
         step(capture=cap)
         torch.cuda.synchronize()
         rows = cap["logits"][:nseq * T]
         seq_temps = state["temps"][:nseq].clone()
         rtemps = seq_temps.repeat_interleave(T)
         stats = softmax_stats(rows, rtemps)
+        lazy = cap["stats"][:nseq * T]
+        visited = ~torch.isnan(lazy[:, 0])
+        stats[visited] = lazy[visited]
         P = softmax_from_stats(rows, rtemps, stats).cpu().numpy()
         Pref = osamp.temperature_softmax(rows.float().cpu().numpy(), rtemps.cpu().numpy())
         softmax_ok = bool(np.allclose(P, Pref, rtol=1e-5, atol=1e-35))
@@ -458,6 +466,11 @@ def integrated_parity(args, torch, state, step, nseq):
         okv.kv_compact(k_ref, v_ref, bt_local, vb.ctx[:nseq], gpu["path"], gpu["acc"], 256)
         kv_ok = bool(np.array_equal(after[0], k_ref) and np.array_equal(after[1], v_ref))
         moved = int(np.clip(gpu["acc"], 0, None).sum())
+        want_vis = np.zeros(nseq * T, bool)
+        for b in range(nseq):
+            if seq_temps[b].item() > 0:
+                want_vis[b * T + gpu["path"][b, :gpu["acc"][b] + 1]] = True
+        visited_ok = bool(np.array_equal(visited.cpu().numpy(), want_vis))
     finally:
         restore()
     return {"path": bool(np.array_equal(gpu["path"], ref_path)),
@@ -465,6 +478,7 @@ def integrated_parity(args, torch, state, step, nseq):
             "tokens": bool(np.array_equal(gpu["out_tokens"], ref_tok)),
             "next_token": bool(np.array_equal(gpu["next_token"], ref_next)),
             "kv_compact": kv_ok, "softmax_within_1e-5": softmax_ok,
+            "lazy_stats_rows_are_paths": visited_ok,
             "accepted": [int(a) for a in gpu["acc"]],
             "greedy": [bool(g) for g in greedy],
             "planted_path_len": [len(p) - 1 for p in paths],
@@ -573,7 +587,8 @@ def run_kernels(args):
     from nanovllm import _C
     from nanovllm.layers.attention import store_kvcache, tree_attention
     from nanovllm.layers.sampler import (rejection_sample_chain, rejection_sample_tree,
-                                         rejection_sample_tree_logits, softmax_from_stats,
+                                         rejection_sample_tree_logits,
+                                         rejection_sample_tree_logits_lazy, softmax_from_stats,
                                          softmax_stats, temperature_softmax, topk_logprobs)
     from nanovllm.spec.kv_compact import kv_compact
     from nanovllm.spec.ngram import ngram_propose
@@ -789,6 +804,25 @@ def run_kernels(args):
          "outputs compared with the walk on the probabilities of the same statistics", ok,
          "latency-bound walk: reads the logits (and Q) rows it visits")
 
+    # the same walk with lazy statistics: no statistics pass, the walk computes the
+    # statistics of the rows it visits
+    us = gpu_us(lambda: rejection_sample_tree_logits_lazy(logits, rtemps, Qt, toks, parents, Ut,
+                                                          Uft), _C.TIMER_REJECTION)
+    so = torch.full((N, 2), float("nan"), device=dev)
+    lazy = rejection_sample_tree_logits_lazy(logits, rtemps, Qt, toks, parents, Ut, Uft,
+                                             stats_out=so)
+    vis = ~torch.isnan(so[:, 0])
+    st2 = st.clone()
+    st2[vis] = so[vis]
+    Pst = softmax_from_stats(logits, rtemps, st2).view(B, T, V)
+    want = rejection_sample_tree(Pst, Qt, toks, parents, Ut, Uft)
+    ok = all(torch.equal(a, b_) for a, b_ in zip(lazy[:4], want))
+    del Pst
+    emit("rejection_sample_tree_logits_lazy", f"batch 64, 64-node depth-8 trees, vocab {V}: the "
+         f"walk on bf16 logits computing the statistics of the rows it visits", us, None, None,
+         "outputs compared with the walk on the probabilities of the statistics it reports", ok,
+         f"replaces the statistics pass ({int(vis.sum())} of {N} rows visited) plus the walk")
+
     rows = 2048
     us = gpu_us(lambda: topk_logprobs(logits[:rows], 8), _C.TIMER_TOPK)
     lp, tk = topk_logprobs(logits[:rows], 8)
@@ -838,9 +872,8 @@ def main():
     verified = accepted + args.steps * args.batch
     _C.timing_enable(False)
     timers = {k: _C.timing_read(i) for k, i in (
-        ("tree_attention", _C.TIMER_TREE_ATTENTION), ("softmax_stats", _C.TIMER_SOFTMAX),
-        ("rejection", _C.TIMER_REJECTION), ("kv_compact", _C.TIMER_KV_COMPACT),
-        ("store_kvcache", _C.TIMER_STORE_KV))}
+        ("tree_attention", _C.TIMER_TREE_ATTENTION), ("rejection", _C.TIMER_REJECTION),
+        ("kv_compact", _C.TIMER_KV_COMPACT), ("store_kvcache", _C.TIMER_STORE_KV))}
     print(f"[bench] timed {args.steps} steps in {elapsed:.3f}s", file=sys.stderr, flush=True)
 
     vb, cfg = state["vb"], state["cfg"]
@@ -853,21 +886,21 @@ def main():
     attn_ms = avg("tree_attention")
     attn_gbs = attn_bytes / (attn_ms * 1e-3) / 1e9
     traffic, traffic_note = read_pmc_traffic()
-    # The sampler is fused: one pass reads the bf16 logits for the row statistics
-    # (nvx_softmax_stats), then the walk recomputes the probabilities of the rows it
-    # visits; no fp32 probability rows are written.  Algorithmic bytes: the statistics
-    # pass reads every logits row once; each residual pass of the walk reads one bf16
-    # logits row and one fp32 draft row, and a walk that ends at a leaf reads the
-    # leaf's logits row for the final draw.
-    stats_bytes = float(B * T) * V * 2
-    stats_ms = avg("softmax_stats")
-    stats_gbs = stats_bytes / (stats_ms * 1e-3) / 1e9
+    # The sampler is one kernel: the tree walk computes the softmax statistics of each
+    # target row it visits (the accepted path of every sequence) and recomputes every
+    # probability it reads from the bf16 logits; no statistics pass over all rows and
+    # no fp32 probability rows.  Algorithmic bytes: each visited logits row once, plus
+    # one bf16 logits row and one fp32 draft row per residual pass (a rejected child);
+    # the final draw reads a row the walk has visited.
     parents_np = state["parents"].cpu().numpy()
     rows = [walk_rows(parents_np, o.numpy()) for o in outs]
-    walk_bytes = sum(pr * V * 2 + qr * V * 4 for pr, qr in rows) / len(rows)
+    visited = sum(float((o[:, 0] + 1).sum()) for o in outs) / len(outs)
+    resid = sum(qr for _, qr in rows) / len(rows)
+    stats_bytes = visited * V * 2
+    walk_bytes = resid * V * (2 + 4)
     walk_ms = avg("rejection")
     sampler_bytes = stats_bytes + walk_bytes
-    sampler_gbs = sampler_bytes / ((stats_ms + walk_ms) * 1e-3) / 1e9
+    sampler_gbs = sampler_bytes / (walk_ms * 1e-3) / 1e9
 
     out = {
         "metric": METRIC,
@@ -893,17 +926,16 @@ def main():
                      "traffic": traffic, "algorithmic_bytes": attn_bytes,
                      "avg_launch_us": attn_ms * 1e3, "launches": timers["tree_attention"][1],
                      **({"traffic_note": traffic_note} if traffic_note else {})},
-        "sampler": {"path": "fused: row statistics in one read of the bf16 logits, then the tree "
-                            "walk recomputes the probabilities of the rows it visits",
-                    "stats_avg_us": stats_ms * 1e3, "stats_bytes": stats_bytes,
-                    "stats_GBs": stats_gbs, "stats_frac": stats_gbs / HBM_PEAK_GBS,
+        "sampler": {"path": "one kernel: the tree walk computes the softmax statistics of the "
+                            "target rows it visits (exact max, sum in its canonical order) and "
+                            "recomputes each probability it reads from the bf16 logits",
                     "walk_avg_us": walk_ms * 1e3,
-                    "walk_bytes_per_step": walk_bytes,
-                    "walk_rows_per_step": [sum(r[0] for r in rows) / len(rows),
-                                           sum(r[1] for r in rows) / len(rows)],
-                    "walk_GBs": walk_bytes / (walk_ms * 1e-3) / 1e9,
+                    "visited_rows_per_step": visited,
+                    "residual_passes_per_step": resid,
+                    "stats_bytes_per_step": stats_bytes,
+                    "residual_bytes_per_step": walk_bytes,
                     "bytes_per_step": sampler_bytes,
-                    "us_per_step": (stats_ms + walk_ms) * 1e3,
+                    "us_per_step": walk_ms * 1e3,
                     "GBs": sampler_gbs, "frac": sampler_gbs / HBM_PEAK_GBS},
         "kernels_us_per_step": {k: v[0] / args.steps * 1e3 for k, v in timers.items()},
     }

@@ -253,6 +253,31 @@ int nvx_rejection_sample_tree_logits(const void* logits, int32_t logits_dtype,
                                      int32_t* next_token, void* workspace,
                                      size_t workspace_bytes, void* stream);
 
+/* nvx_rejection_sample_tree_logits_lazy: the fused walk without the statistics pass.
+ * On reaching a node the walk computes its row's statistics itself, only for the rows
+ * it visits: stats[2r] = max_y(logit[y]) * log2(e)/T (exact), then stats[2r+1] = 1 / the
+ * sum of exp2(fma(logit[y], log2(e)/T, -stats[2r])) in the walk's canonical order (the
+ * same bits for every number of workgroups per sequence).  stats_out ([num_rows, 2]
+ * fp32, 8-byte aligned, or NULL) receives them for the visited rows; other rows are
+ * left as they were.  Rows at temperature 0 (greedy sequences) need no statistics.
+ * Outputs are bit for bit those of nvx_rejection_sample_tree on the rows
+ * nvx_softmax_from_stats writes from any stats that hold stats_out's values on the
+ * visited rows.  It replaces nvx_softmax_stats + nvx_rejection_sample_tree_logits
+ * where only the walk's outputs are needed (the verify step).  Other arguments and
+ * outputs as nvx_rejection_sample_tree_logits.
+ */
+int nvx_rejection_sample_tree_logits_lazy(const void* logits, int32_t logits_dtype,
+                                          int64_t logits_row_stride, const float* temperatures,
+                                          float* stats_out, const float* draft_probs,
+                                          int64_t q_seq_stride, int32_t vocab,
+                                          const int32_t* tokens, const int32_t* parents,
+                                          const int32_t* num_nodes, int32_t node_stride,
+                                          const float* uniforms, const float* final_uniforms,
+                                          const uint8_t* greedy, int32_t draft_mode,
+                                          int32_t num_seqs, int32_t* path, int32_t* accepted_len,
+                                          int32_t* out_tokens, int32_t* next_token,
+                                          void* workspace, size_t workspace_bytes, void* stream);
+
 /* -------------------------------------------------- fused model layers --
  * Elementwise layers of the target model around the verify-path attention, each
  * one pass over HBM (bf16 in/out, fp32 math).  Not part of the four verify-path

@@ -421,6 +421,7 @@ struct LogitRow {
 };
 
 struct ProbSource {
+  static constexpr bool kLazy = false;
   const float* P;
   int64_t seq_stride;
   int V;
@@ -431,6 +432,7 @@ struct ProbSource {
 
 template <typename VT>
 struct LogitSource {
+  static constexpr bool kLazy = false;
   const VT* L;
   int64_t row_stride;  // elements between logits rows; sequence b's node i is row b*rows_per_seq + i
   int rows_per_seq;
@@ -441,6 +443,36 @@ struct LogitSource {
     const float T = temps[r];
     const float2 st = stats[r];
     return {L + r * row_stride, 1.4426950408889634f / T, st.x, st.y, T == 0.f};
+  }
+};
+
+// Logits whose row statistics the walk computes itself, for the rows it visits only:
+// on arriving at a node, the exact row max of the logits (times log2(e)/T) and then
+// the canonical-order sum of exp2(fma(x, log2(e)/T, -max)) (the walk's own chain,
+// the same bits for every number of workgroups per sequence).  The statistics of each
+// visited row are written to stats_out (when given), so nvx_softmax_from_stats can
+// rebuild exactly the probabilities the walk used.
+template <typename VT>
+struct LazyLogitSource {
+  static constexpr bool kLazy = true;
+  const VT* L;
+  int64_t row_stride;
+  int rows_per_seq;
+  const float* temps;  // per logits row
+  float2* stats_out;   // per logits row, written for visited rows (may be null)
+  __device__ __forceinline__ int64_t index(int b, int cur) const {
+    return (int64_t)b * rows_per_seq + cur;
+  }
+  __device__ __forceinline__ float scale(int b, int cur) const {
+    return 1.4426950408889634f / temps[index(b, cur)];
+  }
+  // the row's raw logits (for the max)
+  __device__ __forceinline__ LogitRow<VT> raw_row(int b, int cur) const {
+    return {L + index(b, cur) * row_stride, 0.f, 0.f, 0.f, true};
+  }
+  __device__ __forceinline__ LogitRow<VT> row(int b, int cur, float M, float inv) const {
+    const float T = temps[index(b, cur)];
+    return {L + index(b, cur) * row_stride, 1.4426950408889634f / T, M, inv, T == 0.f};
   }
 };
 
@@ -850,6 +882,32 @@ __device__ int walk_argmax(const PRow& row, int V, bool vec, float* red, int* re
   return bi == INT32_MAX ? 0 : bi;
 }
 
+// Largest value of the sequence's row (this workgroup's logical waves, then across
+// the sequence's workgroups).  The max is exact in any order.
+template <int NW, int M, typename PRow>
+__device__ float walk_rowmax(const PRow& row, int V, bool vec, float* red, uint32_t* s_x, Coop& co) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const Layout lay(V);
+  float m = -INFINITY;
+  const int lw0 = (co.k * NW + wave) * M;
+  for (int j = lay.lo(lw0); j < lay.hi(lw0 + M - 1); ++j) {
+    const int y0 = j * kSub + lane * 8;
+    if (y0 >= V) break;
+    float p[8];
+    row.load8(y0, V, vec, p);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (y0 + e < V) m = fmaxf(m, p[e]);
+  }
+  m = nvx::block_max<NW * 64>(m, red);
+  if (NW * M < kLW) {
+    if (threadIdx.x == 0) s_x[co.k] = __float_as_uint(m);
+    co.exchange(s_x, co.k, 1, co.K);
+    for (int r = 0; r < co.K; ++r) m = fmaxf(m, __uint_as_float(s_x[r]));
+  }
+  return m;
+}
+
 struct WalkArgs {
   const float* Q;
   int64_t q_seq_stride;
@@ -926,8 +984,11 @@ void rejection_walk_kernel(Src src, WalkArgs a) {
     u_l = a.U[nb + lane];
   }
   // only children of an earlier node are ever tested (the walk moves to higher indices)
-  if (!greedy && lane >= 1 && lane < T && par_l >= 0 && par_l < lane && tok_l >= 0 && tok_l < V) {
-    px_l = src.row(b, par_l).at(tok_l);
+  const bool tested =
+      !greedy && lane >= 1 && lane < T && par_l >= 0 && par_l < lane && tok_l >= 0 && tok_l < V;
+  if (tested) {
+    // with lazy statistics p(x) is read when the walk reaches the parent
+    if constexpr (!Src::kLazy) px_l = src.row(b, par_l).at(tok_l);
     if (!dmode) qx_l = a.Q[(int64_t)b * a.q_seq_stride + (int64_t)par_l * V + tok_l];
   }
   if (threadIdx.x < T) s_tok[threadIdx.x] = tok_l;
@@ -940,7 +1001,31 @@ void rejection_walk_kernel(Src src, WalkArgs a) {
   int cur = 0, depth = 0, next = 0;
   bool owner = co.k == 0;
   while (true) {
-    const auto prow = src.row(b, cur);
+    const auto prow = [&]() {
+      if constexpr (Src::kLazy) {
+        // the statistics of this node's row, computed on arrival: the exact max, then
+        // the canonical sum of exp2(fma(x, a, -max)); greedy rows pass the logits
+        // through and need none
+        float Mx = 0.f, inv = 0.f;
+        const float sc = src.scale(b, cur);
+        if (!greedy && __builtin_isfinite(sc)) {
+          Mx = walk_rowmax<NW, M>(src.raw_row(b, cur), V, vp, red, s_x, co) * sc;
+          float ends_s[M], wpre_s;
+          const PassSpec ps{kPlain, 0.f, nullptr, 0};
+          const float sum = chain_pass<kPlain, NW, M>(src.row(b, cur, Mx, 1.f), nullptr, V, vp, vq, ps,
+                                                      t_lds, ends_s, &wpre_s, co);
+          __syncthreads();  // t_lds read by every thread before it can change
+          inv = 1.f / sum;
+          if (co.k == 0 && threadIdx.x == 0 && src.stats_out)
+            src.stats_out[src.index(b, cur)] = make_float2(Mx, inv);
+        }
+        const auto r = src.row(b, cur, Mx, inv);
+        if (tested && par_l == cur) px_l = r.at(tok_l);
+        return r;
+      } else {
+        return src.row(b, cur);
+      }
+    }();
     const float* qrow = a.Q ? a.Q + (int64_t)b * a.q_seq_stride + (int64_t)cur * V : nullptr;
     uint64_t kids = __ballot(par_l == cur && lane > cur);
     int accepted = -1;
@@ -1360,6 +1445,62 @@ extern "C" int nvx_rejection_sample_tree_logits(
   else
     NVX_HIP(launch_walk(LogitSource<float>{(const float*)logits, logits_row_stride, node_stride,
                                            temperatures, st},
+                        wa, num_seqs, s));
+  return NVX_OK;
+}
+
+extern "C" int nvx_rejection_sample_tree_logits_lazy(
+    const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
+    const float* temperatures, float* stats_out, const float* draft_probs, int64_t q_seq_stride,
+    int32_t vocab, const int32_t* tokens, const int32_t* parents, const int32_t* num_nodes,
+    int32_t node_stride, const float* uniforms, const float* final_uniforms, const uint8_t* greedy,
+    int32_t draft_mode, int32_t num_seqs, int32_t* path, int32_t* accepted_len,
+    int32_t* out_tokens, int32_t* next_token, void* workspace, size_t workspace_bytes,
+    void* stream) {
+  nvx::clear_error();
+  NVX_CHECK(logits_dtype == NVX_DTYPE_F32 || logits_dtype == NVX_DTYPE_BF16,
+            "rejection_sample_tree_logits_lazy: logits must be fp32 or bf16 (dtype code %d)",
+            logits_dtype);
+  NVX_CHECK(num_seqs >= 0 && vocab >= 1 && logits_row_stride >= vocab,
+            "rejection_sample_tree_logits_lazy: bad sizes (seqs=%d, vocab=%d, stride=%lld)",
+            num_seqs, vocab, (long long)logits_row_stride);
+  NVX_CHECK(node_stride >= 1 && node_stride <= kMaxNodes,
+            "rejection_sample_tree_logits_lazy: node_stride must be in [1, %d] (got %d)", kMaxNodes,
+            node_stride);
+  NVX_CHECK(draft_mode == 0 || draft_mode == 1,
+            "rejection_sample_tree_logits_lazy: draft_mode must be 0 or 1");
+  NVX_CHECK(draft_mode == 1 || draft_probs != nullptr,
+            "rejection_sample_tree_logits_lazy: draft_probs required in draft_mode 0");
+  if (num_seqs == 0) return NVX_OK;
+  NVX_CHECK(logits && temperatures && tokens && parents && uniforms && final_uniforms && path &&
+                accepted_len && out_tokens && next_token,
+            "rejection_sample_tree_logits_lazy: null pointer");
+  NVX_CHECK(stats_out == nullptr || aligned8(stats_out),
+            "rejection_sample_tree_logits_lazy: stats_out must be 8-byte aligned");
+  NVX_CHECK(vocab <= kMaxVocab, "rejection_sample_tree_logits_lazy: vocab %d exceeds %d", vocab,
+            kMaxVocab);
+  uint64_t* ex = nullptr;
+  if (!walk_exchange("rejection_sample_tree_logits_lazy", workspace, workspace_bytes, num_seqs,
+                     &ex))
+    return NVX_EINVAL;
+  hipStream_t s = (hipStream_t)stream;
+  nvx::TimerScope timer(NVX_TIMER_REJECTION, s);
+  const bool bf16 = logits_dtype == NVX_DTYPE_BF16;
+  const int per = bf16 ? 8 : 4;  // elements per 16 bytes
+  const bool vp = vocab % per == 0 && logits_row_stride % per == 0 && aligned16(logits);
+  const bool vq = draft_mode == 1 ||
+                  (vocab % 4 == 0 && q_seq_stride % 4 == 0 && aligned16(draft_probs));
+  float2* st = reinterpret_cast<float2*>(stats_out);
+  const WalkArgs wa{draft_mode == 1 ? nullptr : draft_probs, q_seq_stride, vocab, tokens, parents,
+                    num_nodes, node_stride, uniforms, final_uniforms, greedy, draft_mode, path,
+                    accepted_len, out_tokens, next_token, vp, vq, ex};
+  if (bf16)
+    NVX_HIP(launch_walk(LazyLogitSource<uint16_t>{(const uint16_t*)logits, logits_row_stride,
+                                                  node_stride, temperatures, st},
+                        wa, num_seqs, s));
+  else
+    NVX_HIP(launch_walk(LazyLogitSource<float>{(const float*)logits, logits_row_stride,
+                                               node_stride, temperatures, st},
                         wa, num_seqs, s));
   return NVX_OK;
 }

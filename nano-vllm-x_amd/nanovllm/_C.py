@@ -58,6 +58,11 @@ _SIGS = {
                                           c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p,
                                           c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
                                           c_void_p], c_int32),
+    "nvx_rejection_sample_tree_logits_lazy": ([c_void_p, c_int32, c_int64, c_void_p, c_void_p,
+                                               c_void_p, c_int64, c_int32, c_void_p, c_void_p,
+                                               c_void_p, c_int32, c_void_p, c_void_p, c_void_p,
+                                               c_int32, c_int32, c_void_p, c_void_p, c_void_p,
+                                               c_void_p, c_void_p, c_size_t, c_void_p], c_int32),
     "nvx_topk_logprobs": ([c_void_p, c_int32, c_int64, c_int32, c_int32, c_int32, c_void_p,
                            c_void_p, c_void_p], c_int32),
     "nvx_rejection_walk_max_width": ([c_int32], c_int32),

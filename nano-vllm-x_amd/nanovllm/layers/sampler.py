@@ -230,6 +230,59 @@ def rejection_sample_tree_logits(logits, temperatures, stats, draft_probs, token
     return path, acc, out_tokens, nxt
 
 
+def rejection_sample_tree_logits_lazy(logits, temperatures, draft_probs, tokens, parents, uniforms,
+                                      final_uniforms, greedy=None, num_nodes=None,
+                                      draft_mode="stochastic", workspace=None, stats_out=None):
+    """rejection_sample_tree on logits [B*T, V] (row b*T + i for node i of sequence b) and
+    their temperatures [B*T], with no separate statistics pass: the walk computes the
+    softmax statistics of the rows it visits (exact row max, then the sum in its
+    canonical order) and writes them to stats_out (fp32 [B*T, 2], when given; rows the
+    walk does not visit are left as they were).  The results equal
+    rejection_sample_tree(softmax_from_stats(logits, temperatures, stats)) for any stats
+    that hold stats_out's values on the visited rows.  Returns (path, accepted_len,
+    out_tokens, next_token, stats_out)."""
+    B, T = tokens.shape
+    if not stats_eligible(logits) or logits.shape[0] != B * T:
+        raise ValueError("rejection_sample_tree_logits_lazy: logits must be [B*T, V] "
+                         "(see stats_eligible)")
+    V = logits.shape[1]
+    delta = draft_mode == "delta"
+    if not delta:
+        if draft_probs is None or draft_probs.dtype != torch.float32 or \
+                draft_probs.stride(2) != 1 or draft_probs.stride(1) != V or draft_probs.shape[2] != V:
+            raise ValueError("rejection_sample_tree_logits_lazy: draft_probs must be fp32 "
+                             "[B, T', V] with contiguous rows")
+    if T > 64:
+        raise ValueError("rejection_sample_tree_logits_lazy: at most 64 nodes per tree")
+    dev = logits.device
+    temperatures = temperatures.to(device=dev, dtype=torch.float32).contiguous()
+    if temperatures.numel() != B * T:
+        raise ValueError("rejection_sample_tree_logits_lazy: one temperature per logits row")
+    if stats_out is not None and (stats_out.shape != (B * T, 2) or stats_out.dtype != torch.float32
+                                  or not stats_out.is_contiguous()):
+        raise ValueError("rejection_sample_tree_logits_lazy: stats_out must be contiguous fp32 "
+                         "[B*T, 2]")
+    tokens, parents = _i32(tokens), _i32(parents)
+    uniforms = uniforms.to(torch.float32).contiguous()
+    final_uniforms = final_uniforms.to(torch.float32).contiguous()
+    g = None if greedy is None else greedy.to(device=dev, dtype=torch.uint8).contiguous()
+    nn_ = None if num_nodes is None else _i32(num_nodes)
+    path = torch.empty(B, T, dtype=torch.int32, device=dev)
+    acc = torch.empty(B, dtype=torch.int32, device=dev)
+    out_tokens = torch.empty(B, T, dtype=torch.int32, device=dev)
+    nxt = torch.empty(B, dtype=torch.int32, device=dev)
+    _C.require_cuda(logits, temperatures, draft_probs, tokens, parents, uniforms, final_uniforms,
+                    g, nn_, workspace, stats_out)
+    ws, ws_bytes = walk_workspace(B, dev, workspace)
+    _C.check(_C.lib().nvx_rejection_sample_tree_logits_lazy(
+        _C.ptr(logits), _DTYPE_CODE[logits.dtype], logits.stride(0), _C.ptr(temperatures),
+        _C.ptr(stats_out), None if delta else _C.ptr(draft_probs),
+        0 if delta else draft_probs.stride(0), V, _C.ptr(tokens), _C.ptr(parents), _C.ptr(nn_), T,
+        _C.ptr(uniforms), _C.ptr(final_uniforms), _C.ptr(g), 1 if delta else 0, B, _C.ptr(path),
+        _C.ptr(acc), _C.ptr(out_tokens), _C.ptr(nxt), _C.ptr(ws), ws_bytes, _C.stream_of(logits)))
+    return path, acc, out_tokens, nxt, stats_out
+
+
 def rejection_sample_chain(target_probs, draft_probs, draft_token_ids, uniforms, final_uniforms,
                            greedy=None):
     """Chain speculative sampling (Leviathan et al. 2023, Alg. 1).
@@ -271,23 +324,35 @@ class Sampler(nn.Module):
 
 
 class RejectionSampler(nn.Module):
-    """Temperature softmax of the target logits followed by tree verification (fused
-    when the logits qualify: softmax statistics, then a walk that recomputes the
-    probabilities it reads; otherwise temperature_softmax then rejection_sample_tree).
+    """Temperature softmax of the target logits followed by tree verification.  When the
+    logits qualify (stats_eligible) the softmax is fused into the walk: the walk
+    computes the statistics of the rows it visits and recomputes each probability it
+    reads (rejection_sample_tree_logits_lazy; lazy=False instead runs one statistics
+    pass over every row first, softmax_stats + rejection_sample_tree_logits).
+    Otherwise temperature_softmax then rejection_sample_tree.
 
     forward(target_logits [B*T, V], temperatures [B], draft_probs [B, T, V] | None,
-    tokens [B, T], parents [B, T], uniforms [B, T], final_uniforms [B]) ->
-    (path, accepted_len, out_tokens, next_token), int32.
+    tokens [B, T], parents [B, T], uniforms [B, T], final_uniforms [B], num_nodes=None,
+    stats_out=None) -> (path, accepted_len, out_tokens, next_token), int32.  stats_out
+    (fp32 [B*T, 2]) receives the statistics of the visited rows on the lazy path.
     """
 
+    def __init__(self, lazy=True):
+        super().__init__()
+        self.lazy = lazy
+
     def forward(self, target_logits, temperatures, draft_probs, tokens, parents, uniforms,
-                final_uniforms, num_nodes=None):
+                final_uniforms, num_nodes=None, stats_out=None):
         B, T = tokens.shape
         V = target_logits.shape[-1]
         temps = temperatures.to(device=target_logits.device, dtype=torch.float32)
         rows = target_logits.view(B * T, V)
         row_temps = temps.repeat_interleave(T)
         mode = "delta" if draft_probs is None else "stochastic"
+        if stats_eligible(rows) and self.lazy:
+            return rejection_sample_tree_logits_lazy(rows, row_temps, draft_probs, tokens, parents,
+                                                     uniforms, final_uniforms, temps == 0,
+                                                     num_nodes, mode, stats_out=stats_out)[:4]
         if stats_eligible(rows):
             # fused: one statistics pass over the logits, then the walk recomputes the
             # probabilities of the rows it visits (no fp32 probability rows written)

@@ -10,8 +10,8 @@ import torch
 from nanovllm import _C
 from nanovllm.layers.sampler import (RejectionSampler, Sampler, rejection_sample_chain,
                                      rejection_sample_tree, rejection_sample_tree_logits,
-                                     softmax_from_stats, softmax_stats, stats_eligible,
-                                     temperature_softmax)
+                                     rejection_sample_tree_logits_lazy, softmax_from_stats,
+                                     softmax_stats, stats_eligible, temperature_softmax)
 from nanovllm.spec.tree import chain_parents, random_tree
 from oracle import sampler as osamp
 
@@ -289,6 +289,43 @@ def test_sampler_distribution(dev):
     assert (tg == V - 1).all()
 
 
+def check_lazy(ld, rtd, stats, args, greedy, Qn, toks, parents, U, Uf, delta):
+    """The walk with lazy statistics against the oracle: it must visit exactly the
+    accepted path of every sampled sequence (and no row of a greedy one), its statistics
+    must match float64 (1e-5 relative), and its outputs must equal the oracle's walk on
+    the probabilities softmax_from_stats rebuilds from those statistics (bit-exact).
+    stats: any statistics for the rows it does not visit."""
+    BT, V = ld.shape
+    B = len(greedy)
+    T = BT // B
+    so_d = torch.full((BT, 2), float("nan"), device=ld.device)
+    lazy = rejection_sample_tree_logits_lazy(ld, rtd, *args, stats_out=so_d)
+    path, acc = lazy[0].cpu().numpy(), lazy[1].cpu().numpy()
+    so = so_d.cpu().numpy()
+    visited = ~np.isnan(so[:, 0])
+    want = np.zeros(BT, bool)
+    for b in range(B):
+        if not greedy[b]:
+            want[b * T + path[b, :acc[b] + 1]] = True
+    assert np.array_equal(visited, want), "lazy walk visited other rows than its paths"
+    x = ld[torch.from_numpy(np.nonzero(visited)[0]).to(ld.device)].float().cpu().numpy()
+    x = x.astype(np.float64)
+    a = 1.4426950408889634 / rtd.cpu().numpy()[visited].astype(np.float64)
+    M = x.max(1) * a
+    S = np.exp2(x * a[:, None] - M[:, None]).sum(1)
+    np.testing.assert_allclose(so[visited, 0], M, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(so[visited, 1], 1.0 / S, rtol=1e-5)
+    st = stats.clone()
+    vis_d = torch.from_numpy(visited).to(ld.device)
+    st[vis_d] = so_d[vis_d]
+    P = softmax_from_stats(ld, rtd, st).cpu().numpy().reshape(B, T, V)
+    ref = osamp.rejection_sample_tree(P, None if delta else Qn, toks, parents, U, Uf, greedy, None,
+                                      delta)
+    for name, a_, r in zip(("path", "accepted_len", "out_tokens", "next_token"), lazy[:4], ref):
+        assert np.array_equal(a_.cpu().numpy(), r), f"{name}: lazy walk != oracle"
+    return lazy
+
+
 def fused_case(dev, B, T, V, depth, seed, dtype=torch.bfloat16, delta=False, greedy_frac=0.0,
                temp=0.8):
     """Fused sampler (softmax_stats + rejection_sample_tree_logits) against the walk on
@@ -341,6 +378,8 @@ def fused_case(dev, B, T, V, depth, seed, dtype=torch.bfloat16, delta=False, gre
     np.testing.assert_allclose(st[live, 0], M[live], rtol=1e-5, atol=1e-6)
     np.testing.assert_allclose(st[live, 1], 1.0 / S[live], rtol=1e-5)
     assert (st[~live] == 0).all()
+    check_lazy(ld, rtd, stats, args, greedy, None if delta else Qn, toks, parents, U.numpy(),
+               Uf.numpy(), delta)
     return fused
 
 
@@ -362,9 +401,9 @@ def test_fused_sampler_delta_and_deep_trees(dev):
 
 @pytest.mark.gpu
 def test_rejection_sampler_module_paths(dev):
-    """RejectionSampler takes the fused path for eligible logits (equal to the walk on
-    softmax_from_stats) and the two-step path otherwise (equal to the walk on
-    temperature_softmax)."""
+    """RejectionSampler takes the lazy fused path for eligible logits (equal to the walk
+    on softmax_from_stats of the statistics it reports; lazy=False: of softmax_stats) and
+    the two-step path otherwise (equal to the walk on temperature_softmax)."""
     for V in (4096, 1001):  # 1001: not a multiple of 8, two-step path
         rng = np.random.default_rng(V)
         g = torch.Generator().manual_seed(V)
@@ -377,10 +416,22 @@ def test_rejection_sampler_module_paths(dev):
         Uf = torch.from_numpy(rng.random(B).astype(np.float32)).to(dev)
         temps = torch.tensor([0.7, 0.0, 1.0, 1.3, 0.9], device=dev)
         assert stats_eligible(logits) == (V == 4096)
-        got = RejectionSampler()(logits, temps, Q, toks, parents, U, Uf)
         rt = temps.repeat_interleave(T)
+        so = torch.zeros(B * T, 2, device=dev)
+        got = RejectionSampler()(logits, temps, Q, toks, parents, U, Uf, stats_out=so)
         if V == 4096:
-            P = softmax_from_stats(logits, rt, softmax_stats(logits, rt)).view(B, T, V)
+            st = softmax_stats(logits, rt)
+            eager = RejectionSampler(lazy=False)(logits, temps, Q, toks, parents, U, Uf)
+            want = rejection_sample_tree(softmax_from_stats(logits, rt, st).view(B, T, V), Q, toks,
+                                         parents, U, Uf, temps == 0)
+            for a, b_ in zip(eager, want):
+                assert torch.equal(a, b_)
+            path, acc = got[0].cpu().numpy(), got[1].cpu().numpy()
+            for b in range(B):
+                if float(temps[b]) > 0:  # the lazy walk's statistics of its visited rows
+                    rows = torch.from_numpy(b * T + path[b, :acc[b] + 1]).to(dev)
+                    st[rows] = so[rows]
+            P = softmax_from_stats(logits, rt, st).view(B, T, V)
         else:
             P = temperature_softmax(logits, rt).view(B, T, V)
         want = rejection_sample_tree(P, Q, toks, parents, U, Uf, temps == 0)
@@ -433,3 +484,6 @@ def test_fused_sampler_verify8b_batch(dev, delta):
         assert np.array_equal(a.cpu().numpy(), r), f"{name}: fused != oracle"
     if not delta:  # sampled sequences walk several levels deep
         assert ref[1][~greedy].mean() >= 2
+    del P, two
+    check_lazy(logits, row_temps, stats, args, greedy, None if delta else Q.cpu().numpy(),
+               toks.cpu().numpy(), parents, U.cpu().numpy(), Uf.cpu().numpy(), delta)
