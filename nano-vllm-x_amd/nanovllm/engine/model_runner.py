@@ -137,7 +137,7 @@ class ModelRunner:
         self.rejection = RejectionSampler()
         self.allocate_kv_cache()
         self.graphs = {}
-        self.draft_graphs = {}
+        self.eagle_graphs = {}
         self.catchup_graphs = {}
         if not self.enforce_eager:
             self.capture_cudagraph()
@@ -303,13 +303,14 @@ class ModelRunner:
     # Verify / decode steps replay a captured target forward (reference
     # model_runner.py:222-257, there for q_len = 1).  A graph covers bs sequences of
     # T rows each (T = 1 or the longest verify chain, a step using the smallest that
-    # fits its drafts), with static input and context buffers per T; the attention launch is sized for max_model_len, so any context up to
-    # it fits.  Batches are padded to the next captured size with empty sequences
-    # (context 0, slot -1: nothing stored, output rows 0).  The LM head and the
-    # sampler run outside the graph.  With EAGLE-3 the graph is the target's tree
-    # verify (T = tree nodes) and also returns the aux residual streams the draft head
-    # fuses; the draft tree expansion and the draft catch-up are captured per batch
-    # size too.
+    # fits its drafts), with static input and context buffers per T; the attention
+    # launch is sized for max_model_len, so any context up to it fits.  Batches are
+    # padded to the next captured size with empty sequences (context 0, slot -1:
+    # nothing stored, output rows 0).  The LM head and the sampler run outside the
+    # graph.  With EAGLE-3 one graph per batch size holds the whole step up to the
+    # logits: the draft tree expansion, the verify rows built from it on the device,
+    # and the target's tree verify with the aux residual streams the draft head fuses;
+    # the draft catch-up is captured per batch size too.
 
     def _graph_rows(self):
         """Rows per sequence of the captured graphs: the EAGLE-3 tree, or both a plain
@@ -333,47 +334,101 @@ class ModelRunner:
         self.graph_bs = [b for b in [1, 2, 4, 8] + list(range(16, max_bs + 1, 16)) if b <= max_bs]
         self.graph_vars = {}
         pool = None
-        for T in sorted(self._graph_rows(), reverse=True):
-            pool = self._capture_rows(T, max_bs, pool)
-        if self.draft is not None:
-            self._capture_draft_trees(max_bs, pool)
+        if self.draft is None:
+            for T in sorted(self._graph_rows(), reverse=True):
+                pool = self._capture_rows(T, max_bs, pool)
+        else:
+            T = 1 + cfg.num_speculative_tokens
+            self._graph_buffers(T, max_bs)
+            pool = self._capture_eagle_steps(max_bs, pool)
+            self._capture_catch_up(max_bs, pool)
 
-    def _capture_draft_trees(self, max_bs, pool):
-        """Graphs of the EAGLE-3 tree expansion (every draft level, its top-k and the
-        tree selection) per captured batch size, over static inputs.  Padding sequences
-        have context 0, slot -1 and no pages; their trees are discarded.  The draft
-        attention is sized for max_model_len, as the target's."""
+    def _capture_eagle_steps(self, max_bs, pool):
+        """One graph per captured batch size for the EAGLE-3 step up to the target's
+        hidden states: the draft tree expansion (every draft level, its top-k and the
+        tree selection) over static root states, then the verify rows built from the
+        tree on the device (tokens, positions ctx + depth, slots ctx + i, ancestor
+        masks), then the target's tree verify with its aux residual streams.  Inputs
+        are static buffers the step fills (root states, root tokens, cached lengths,
+        block tables, a valid flag per sequence); padding sequences have no pages,
+        context 0 and slot -1.  Both attention launches are sized for max_model_len."""
         cfg = self.config
-        k, depth, T = cfg.eagle_topk, cfg.eagle_depth, 1 + cfg.num_speculative_tokens
-        rmax = k * max(depth - 1, 1)
+        k, T = cfg.eagle_topk, 1 + cfg.num_speculative_tokens
         H = cfg.hf_config.hidden_size
+        gv = self.graph_vars[T]
+        # root token, cached length and valid flag per sequence share one buffer, so a
+        # step fills them with one copy
+        meta = torch.zeros(max_bs, 3, dtype=torch.int64)
         dg = dict(
             root_feat=torch.zeros(max_bs, H),
             root_tok=torch.zeros(max_bs, k, dtype=torch.int64),
             root_lp=torch.zeros(max_bs, k, dtype=torch.float32),
-            ctx=torch.zeros(max_bs, dtype=torch.int64),
-            block_tables=torch.full((max_bs, self.graph_vars[T]["max_blocks"]), -1,
-                                    dtype=torch.int32),
+            meta=meta, roots=meta[:, 0], ctx=meta[:, 1], valid=meta[:, 2],
+            block_tables=torch.full((max_bs, gv["max_blocks"]), -1, dtype=torch.int32),
             tokens=torch.zeros(max_bs, T - 1, dtype=torch.int64),
             parents=torch.zeros(max_bs, T, dtype=torch.int64),
             depths=torch.zeros(max_bs, T, dtype=torch.int64),
             masks=torch.zeros(max_bs, T, dtype=torch.int64),
+            vtok=torch.zeros(max_bs, T, dtype=torch.int32),
+            vpar=torch.zeros(max_bs, T, dtype=torch.int32),
         )
         self.draft_graph_vars = dg
+        # pinned host staging: the step's meta and block tables, and the read-back of
+        # the accepted lengths and tokens
+        host = dict(device="cpu", pin_memory=True)
+        self._pin_meta = torch.zeros(max_bs, 3, dtype=torch.int64, **host)
+        self._pin_bt = torch.full((max_bs, gv["max_blocks"]), -1, dtype=torch.int32, **host)
+        self._pin_acc = torch.zeros(max_bs, dtype=torch.int32, **host)
+        self._pin_out = torch.zeros(max_bs, T, dtype=torch.int32, **host)
         for bs in reversed(self.graph_bs):
-            def expand():
-                outs = self._expand_draft_tree(
-                    dg["root_tok"][:bs], dg["root_lp"][:bs], dg["root_feat"][:bs],
-                    dg["ctx"][:bs], dg["block_tables"][:bs], cfg.max_model_len)
+            def step():
+                ctx_d, bt = dg["ctx"][:bs], dg["block_tables"][:bs]
+                outs = self._expand_draft_tree(dg["root_tok"][:bs], dg["root_lp"][:bs],
+                                               dg["root_feat"][:bs], ctx_d, bt, cfg.max_model_len)
                 for name, t in zip(("tokens", "parents", "depths", "masks"), outs):
                     dg[name][:bs] = t
+                tree_tok, parents, depths, masks = outs
+                tokens = torch.cat([dg["roots"][:bs].unsqueeze(1), tree_tok], dim=1)
+                dg["vtok"][:bs] = tokens
+                dg["vpar"][:bs] = parents
+                h, a = self._verify_tree(tokens, depths, masks, ctx_d, bt, dg["valid"][:bs] != 0,
+                                         cfg.max_model_len)
+                gv["outputs"][:bs * T] = h
+                gv["aux"][:bs * T] = a
 
-            expand()  # warmup
+            step()  # warmup
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, pool):
-                expand()
-            self.draft_graphs[bs] = graph
+                step()
+            if pool is None:
+                pool = graph.pool()
+            self.eagle_graphs[bs] = graph
             torch.cuda.synchronize()
+        return pool
+
+    def _verify_tree(self, tokens, depths, masks, ctx_d, block_tables, valid, max_ctx):
+        """The target's tree verify from device tensors only (capturable): tokens, depths,
+        masks [B, T]; node i at position ctx + depth(i), stored at ctx + i; invalid
+        (padding) sequences have context 0.  Returns (hidden [B*T, H], aux)."""
+        B, T = tokens.shape
+        dev = tokens.device
+        positions = (ctx_d.unsqueeze(1) + depths).reshape(-1)
+        slot_mapping = self._slot_grid(block_tables, ctx_d, T).reshape(-1)
+        context_lens = torch.where(valid, ctx_d + T, 0).to(torch.int32)
+        set_context(False, cu_seqlens_q=torch.arange(0, B * T + 1, T, dtype=torch.int32, device=dev),
+                    max_seqlen_q=T, slot_mapping=slot_mapping, context_lens=context_lens,
+                    block_tables=block_tables, tree_mask=masks.reshape(-1).contiguous(),
+                    max_context_len=max_ctx)
+        try:
+            return self.model(tokens.reshape(-1), positions, self.draft.aux_layers)
+        finally:
+            reset_context()
+
+    def _capture_catch_up(self, max_bs, pool):
+        cfg = self.config
+        k, depth, T = cfg.eagle_topk, cfg.eagle_depth, 1 + cfg.num_speculative_tokens
+        H = cfg.hf_config.hidden_size
+        dg = self.draft_graph_vars
 
         # Draft catch-up per batch size: depth + 1 rows per sequence (the longest
         # accepted path plus the bonus token), rows past a sequence's accepted length
@@ -426,7 +481,8 @@ class ModelRunner:
         reset_context()
         return self._draft_state(normed, feats, seq.squeeze(1) * D1 + acc)
 
-    def _capture_rows(self, T, max_bs, pool):
+    def _graph_buffers(self, T, max_bs):
+        """Static buffers of the captured steps with T rows per sequence."""
         cfg, hf = self.config, self.config.hf_config
         aux_layers = self.draft.aux_layers if self.draft is not None else None
         reserve = max(T, cfg.verify_lookahead)  # slots a step may reserve past the context
@@ -446,6 +502,12 @@ class ModelRunner:
             aux=torch.zeros(rows, len(aux_layers) * hf.hidden_size) if aux_layers else None,
         )
         self.graph_vars[T] = gv
+        return gv
+
+    def _capture_rows(self, T, max_bs, pool):
+        cfg = self.config
+        aux_layers = self.draft.aux_layers if self.draft is not None else None
+        gv = self._graph_buffers(T, max_bs)
         for bs in reversed(self.graph_bs):
             n = bs * T
             set_context(False, cu_seqlens_q=gv["cu_seqlens_q"][:bs + 1], max_seqlen_q=T,
@@ -621,31 +683,53 @@ class ModelRunner:
         reset_context()
         return token_ids
 
+    def _eagle_graphed(self, B):
+        return bool(self.eagle_graphs) and B <= self.graph_bs[-1]
+
+    def _replay_eagle_step(self, seqs, rows, ctx, block_tables=None):
+        """Fill the captured EAGLE-3 step's static inputs and replay it: the root states
+        of the sequences' DraftStates rows (gathered on the device), and root tokens,
+        cached lengths, valid flags and block tables from pinned host staging (one copy
+        each); the batch is padded to the next captured size with empty sequences.  The
+        tree lands in draft_graph_vars, the target's hidden states and aux streams in
+        graph_vars[T].  block_tables: the sequences' padded device tables (only their
+        width is used when given; the staging is built from the sequences)."""
+        B = len(seqs)
+        g = next(b for b in self.graph_bs if b >= B)
+        dg = self.draft_graph_vars
+        st = self.draft_states
+        for name, src in (("root_feat", st.feat), ("root_tok", st.tok), ("root_lp", st.lp)):
+            torch.index_select(src, 0, rows, out=dg[name][:B])
+            if g > B:
+                dg[name][B:g].zero_()
+        meta = self._pin_meta.numpy()
+        meta[:g] = 0
+        meta[:B, 0] = [seq.last_token for seq in seqs]
+        meta[:B, 1] = ctx
+        meta[:B, 2] = 1
+        bt = self._pin_bt.numpy()
+        bt[:g] = -1
+        for i, seq in enumerate(seqs):
+            bt[i, :len(seq.block_table)] = seq.block_table
+        dg["meta"][:g].copy_(self._pin_meta[:g], non_blocking=True)
+        dg["block_tables"][:g].copy_(self._pin_bt[:g], non_blocking=True)
+        self.eagle_graphs[g].replay()
+
     def _eagle_tree(self, seqs, ctx, block_tables, rows=None):
         """Expand one draft tree per sequence from its resident root state (rows: the
         sequences' DraftStates rows, looked up when not given).  Returns tokens
         [B, T-1], parents [B, T], node depths [B, T] and ancestor masks [B, T].
-        Replays the captured expansion when graphs are on and the batch fits."""
+        With graphs on and a batch that fits, replays the captured EAGLE-3 step (which
+        also runs the target's verify of the tree) and returns copies of its tree."""
         B = len(seqs)
         if rows is None:
             rows = self.draft_states.rows([seq.seq_id for seq in seqs])
-        root_feat, root_tok, root_lp = self.draft_states.get(rows)
         ctx_d = _pinned(ctx, torch.int64)
-        if self.draft_graphs and B <= self.graph_bs[-1]:
-            g = next(b for b in self.graph_bs if b >= B)
+        if self._eagle_graphed(B):
+            self._replay_eagle_step(seqs, rows, ctx)
             dg = self.draft_graph_vars
-            dg["root_feat"][:B] = root_feat
-            dg["root_feat"][B:g].zero_()
-            dg["root_tok"][:B] = root_tok
-            dg["root_tok"][B:g].zero_()
-            dg["root_lp"][:B] = root_lp
-            dg["root_lp"][B:g].zero_()
-            dg["ctx"].zero_()
-            dg["ctx"][:B] = ctx_d
-            dg["block_tables"].fill_(-1)
-            dg["block_tables"][:B, :block_tables.shape[1]] = block_tables
-            self.draft_graphs[g].replay()
             return tuple(dg[name][:B].clone() for name in ("tokens", "parents", "depths", "masks"))
+        root_feat, root_tok, root_lp = self.draft_states.get(rows)
         return self._expand_draft_tree(root_tok, root_lp, root_feat, ctx_d, block_tables, max(ctx))
 
     def _expand_draft_tree(self, root_tok, root_lp, root_feat, ctx_d, block_tables, max_ctx):
@@ -686,51 +770,62 @@ class ModelRunner:
         B = len(seqs)
         ctx = [len(seq) - 1 for seq in seqs]
         self._check_pages(seqs, ctx, cfg.verify_lookahead)
-        block_tables = self.prepare_block_tables(seqs)
         rows = self.draft_states.rows([seq.seq_id for seq in seqs])
-        tree_tok, parents, depths, masks = self._eagle_tree(seqs, ctx, block_tables, rows)
-        # target verify of the trees: node i at position ctx + depth(i), stored at ctx + i
-        roots = _pinned([seq.last_token for seq in seqs], torch.int64)
-        tokens = torch.cat([roots.unsqueeze(1), tree_tok], dim=1)            # [B, T]
-        ctx_d = _pinned(ctx, torch.int64)
-        positions = (ctx_d.unsqueeze(1) + depths).reshape(-1)
-        slot_mapping = self._slot_grid(block_tables, ctx_d, T).reshape(-1)
-        context_lens = (ctx_d + T).to(torch.int32)
-        set_context(False, cu_seqlens_q=torch.arange(0, B * T + 1, T, dtype=torch.int32, device="cuda"),
-                    max_seqlen_q=T, slot_mapping=slot_mapping, context_lens=context_lens,
-                    block_tables=block_tables, tree_mask=masks.reshape(-1).contiguous(),
-                    max_context_len=max(ctx) + T)
-        graphed = bool(self.graphs) and B <= self.graph_bs[-1]
+        graphed = self._eagle_graphed(B)
         if graphed:
-            hidden, aux = self.replay_graph(tokens.reshape(-1), positions)
+            # one replay: draft tree expansion, verify rows, target verify with aux
+            self._replay_eagle_step(seqs, rows, ctx)
+            gv, dg = self.graph_vars[T], self.draft_graph_vars
+            hidden, aux = gv["outputs"][:B * T], gv["aux"][:B * T]
+            tok32, par32 = dg["vtok"][:B], dg["vpar"][:B]
+            ctx_d, block_tables = dg["ctx"][:B], dg["block_tables"][:B]
         else:
-            hidden, aux = self.model(tokens.reshape(-1), positions, self.draft.aux_layers)
+            block_tables = self.prepare_block_tables(seqs)
+            ctx_d = _pinned(ctx, torch.int64)
+            tree_tok, parents, depths, masks = self._eagle_tree(seqs, ctx, block_tables, rows)
+            # target verify of the trees: node i at position ctx + depth(i), stored at ctx + i
+            roots = _pinned([seq.last_token for seq in seqs], torch.int64)
+            tokens = torch.cat([roots.unsqueeze(1), tree_tok], dim=1)            # [B, T]
+            valid = torch.ones(B, dtype=torch.bool, device="cuda")
+            hidden, aux = self._verify_tree(tokens, depths, masks, ctx_d, block_tables, valid,
+                                            max(ctx) + T)
+            tok32, par32 = tokens.to(torch.int32), parents.to(torch.int32)
         logits = self.model.compute_logits(hidden)
-        reset_context()
         temperatures = self.prepare_sample(seqs)
         U, Uf = self._uniforms(B, T)
-        tok32, par32 = tokens.to(torch.int32), parents.to(torch.int32)
         path, acc, out_tokens, _ = self.rejection(logits, temperatures, None, tok32, par32, U, Uf)
         ctx32 = ctx_d.to(torch.int32)
-        # a failed walk row (accepted_len -1) compacts nothing; the check after the
-        # read-back raises before the catch-up could take another row as its root
+        # a failed walk row (accepted_len -1) compacts nothing
         kv_compact(self.kv_cache[0], self.kv_cache[1], block_tables, ctx32, path, acc)
-        acc_h = acc.tolist()
-        result = self._verified_tokens(acc_h, out_tokens.tolist())
         # Draft catch-up: rows ctx .. ctx+a take the accepted tokens then the bonus /
         # recovered token, with the target features of the accepted path's tree rows.
-        # After the read-back, so the GPU runs it while the host schedules the next step.
         if graphed and self.catchup_graphs:
-            state = self._replay_catch_up(acc, path, out_tokens, ctx_d, block_tables)
-        else:
-            state = self._catch_up_packed(acc, acc_h, path, out_tokens, ctx, ctx_d, block_tables,
-                                          aux, T)
+            # The read-back is an asynchronous copy into pinned memory with an event
+            # behind it; the captured catch-up is queued after it, so the GPU runs the
+            # catch-up while the host checks the tokens and schedules the next step.  A
+            # failed walk row enters the catch-up with accepted length 0 (clamped on
+            # the device, never -1), and the check after the event raises.
+            acc_h, out_h = self._pin_acc[:B], self._pin_out[:B]
+            acc_h.copy_(acc, non_blocking=True)
+            out_h.copy_(out_tokens, non_blocking=True)
+            landed = torch.cuda.Event()
+            landed.record()
+            state = self._replay_catch_up(acc.clamp(min=0), path, out_tokens, ctx_d, block_tables,
+                                          staged=True)
+            self.draft_states.put(rows, *state)
+            landed.synchronize()
+            return self._verified_tokens(acc_h.tolist(), out_h.tolist())
+        acc_h = acc.tolist()
+        result = self._verified_tokens(acc_h, out_tokens.tolist())
+        state = self._catch_up_packed(acc, acc_h, path, out_tokens, ctx, ctx_d, block_tables,
+                                      aux, T)
         self.draft_states.put(rows, *state)
         return result
 
-    def _replay_catch_up(self, acc, path, out_tokens, ctx_d, block_tables):
+    def _replay_catch_up(self, acc, path, out_tokens, ctx_d, block_tables, staged=False):
         """The captured catch-up (batch padded to a captured size); the target features
-        are the verify graph's aux rows of this step.  Returns views of its outputs."""
+        are the verify graph's aux rows of this step.  staged: the step's replay already
+        filled the cached lengths and block tables.  Returns views of its outputs."""
         B = acc.shape[0]
         g = next(b for b in self.graph_bs if b >= B)
         cg, dg = self.catchup_graph_vars, self.draft_graph_vars
@@ -738,10 +833,11 @@ class ModelRunner:
         for name, src in (("acc", acc), ("path", path[:, :D1]), ("out", out_tokens[:, :D1])):
             cg[name][:B] = src
             cg[name][B:g].zero_()
-        dg["ctx"].zero_()
-        dg["ctx"][:B] = ctx_d
-        dg["block_tables"].fill_(-1)
-        dg["block_tables"][:B, :block_tables.shape[1]] = block_tables
+        if not staged:
+            dg["ctx"].zero_()
+            dg["ctx"][:B] = ctx_d
+            dg["block_tables"].fill_(-1)
+            dg["block_tables"][:B, :block_tables.shape[1]] = block_tables
         self.catchup_graphs[g].replay()
         return cg["feat"][:B], cg["tok"][:B], cg["lp"][:B]
 

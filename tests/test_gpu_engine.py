@@ -142,16 +142,17 @@ def test_eagle3_speculative_greedy_is_target_argmax(dev):
 
 @pytest.mark.gpu
 def test_eagle3_graph_verify_greedy_is_target_argmax(dev):
-    """The target's tree verify (with the aux residual streams) and the draft tree
-    expansion replayed from captured HIP graphs, batches padded to the graph sizes:
-    still the target's argmax."""
+    """The EAGLE-3 step (draft tree expansion, verify rows, the target's tree verify with
+    the aux residual streams) replayed from one captured HIP graph per batch size, and
+    the catch-up from its own, batches padded to the graph sizes: still the target's
+    argmax."""
     V = 64
     llm = LLM("unused", hf_config=tiny_config(vocab=V, layers=6), num_kvcache_blocks=64,
               speculative_method="eagle3", num_speculative_tokens=15, eagle_topk=8, eagle_depth=4,
               max_num_batched_tokens=4096, enforce_eager=False, max_num_seqs=16,
               max_model_len=2048)
-    assert llm.model_runner.graphs and list(llm.model_runner.graph_vars) == [16]
-    assert sorted(llm.model_runner.draft_graphs) == llm.model_runner.graph_bs
+    assert list(llm.model_runner.graph_vars) == [16]
+    assert sorted(llm.model_runner.eagle_graphs) == llm.model_runner.graph_bs
     rng = np.random.default_rng(3)
     ps = [rng.integers(0, V, size=n).tolist() for n in (30, 257, 100)]
     outs = llm.generate(ps, SamplingParams(temperature=0.0, max_tokens=40, ignore_eos=True),
@@ -316,17 +317,17 @@ def test_graph_replays_are_stable(dev):
 
 @pytest.mark.gpu
 def test_eagle3_draft_tree_graph_replays_are_stable(dev):
-    """The captured draft tree expansion, replayed three times for four sequences (a
-    captured batch size, no padding) with eager expansions and synchronisations in
-    between: every replay gives the eager expansion's tree, depths and masks, bit for
-    bit."""
+    """The captured EAGLE-3 step, replayed three times for four sequences (a captured
+    batch size, no padding) with eager steps and synchronisations in between: every
+    replay gives the eager expansion's tree, depths and masks, and the eager target
+    verify's hidden states and aux streams of that tree, bit for bit."""
     V = 64
     llm = LLM("unused", hf_config=tiny_config(vocab=V, layers=2), num_kvcache_blocks=64,
               speculative_method="eagle3", num_speculative_tokens=15, eagle_topk=8, eagle_depth=4,
               max_num_batched_tokens=4096, enforce_eager=False, max_num_seqs=16,
               max_model_len=2048)
     runner, bm, cfg = llm.model_runner, llm.scheduler.block_manager, llm.model_runner.config
-    assert 4 in runner.draft_graphs
+    assert 4 in runner.eagle_graphs
     g = torch.Generator(device="cuda").manual_seed(11)
     for cache in (runner.draft.self_attn.attn.k_cache, runner.draft.self_attn.attn.v_cache):
         cache.normal_(generator=g)
@@ -349,13 +350,24 @@ def test_eagle3_draft_tree_graph_replays_are_stable(dev):
         feat, tok, lp = runner.draft_states.get(runner.draft_states.rows([s.seq_id for s in seqs]))
         ctx_d = torch.tensor(ctx, dtype=torch.int64, device="cuda")
         args = (tok, lp, feat, ctx_d, block_tables, cfg.max_model_len)
+        T = 1 + cfg.num_speculative_tokens
+        roots = torch.tensor([s.last_token for s in seqs], device="cuda")
+        valid = torch.ones(len(seqs), dtype=torch.bool, device="cuda")
+        gv = runner.graph_vars[T]
         for rep in range(3):
             eager = runner._expand_draft_tree(*args)
+            tokens = torch.cat([roots.unsqueeze(1), eager[0]], dim=1)
+            e_h, e_a = runner._verify_tree(tokens, eager[2], eager[3], ctx_d, block_tables, valid,
+                                           cfg.max_model_len)
+            e_h, e_a = e_h.clone(), e_a.clone()
             torch.cuda.synchronize()
             replay = runner._eagle_tree(seqs, ctx, block_tables)
             torch.cuda.synchronize()
             assert len(replay) == len(eager) == 4
             assert all(torch.equal(r, e) for r, e in zip(replay, eager)), f"replay {rep}"
+            n = len(seqs) * T
+            assert torch.equal(gv["outputs"][:n], e_h), f"replay {rep}: verify hidden states"
+            assert torch.equal(gv["aux"][:n], e_a), f"replay {rep}: aux streams"
         e_par = eager[1]
         assert (e_par[:, 0] == -1).all() and (e_par[:, 1:] < torch.arange(1, 16, device="cuda")).all()
     for seq in seqs:
