@@ -140,6 +140,36 @@ def _rejection_sample_tree_logits_fake(logits, temperatures, stats, draft_probs,
             tokens.new_empty((B, T), **i32), tokens.new_empty((B,), **i32))
 
 
+@torch.library.custom_op("nvx::rejection_sample_tree_logits_lazy", mutates_args=())
+def rejection_sample_tree_logits_lazy(logits: Tensor, temperatures: Tensor,
+                                      draft_probs: Optional[Tensor], tokens: Tensor,
+                                      parents: Tensor, uniforms: Tensor, final_uniforms: Tensor,
+                                      greedy: Optional[Tensor] = None,
+                                      num_nodes: Optional[Tensor] = None,
+                                      draft_mode: str = "stochastic"
+                                      ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """The tree walk on logits [B*T, V] computing the softmax statistics of the rows it
+    visits (the verify step's sampler): int32 (path [B, T], accepted_len [B],
+    out_tokens [B, T], next_token [B]) and fp32 stats [B*T, 2] (NaN on rows not
+    visited)."""
+    B, T = tokens.shape
+    stats = torch.full((B * T, 2), float("nan"), dtype=torch.float32, device=logits.device)
+    return _sampler.rejection_sample_tree_logits_lazy(logits, temperatures, draft_probs, tokens,
+                                                      parents, uniforms, final_uniforms, greedy,
+                                                      num_nodes, draft_mode, stats_out=stats)
+
+
+@rejection_sample_tree_logits_lazy.register_fake
+def _rejection_sample_tree_logits_lazy_fake(logits, temperatures, draft_probs, tokens, parents,
+                                            uniforms, final_uniforms, greedy=None, num_nodes=None,
+                                            draft_mode="stochastic"):
+    B, T = tokens.shape
+    i32 = dict(dtype=torch.int32)
+    return (tokens.new_empty((B, T), **i32), tokens.new_empty((B,), **i32),
+            tokens.new_empty((B, T), **i32), tokens.new_empty((B,), **i32),
+            logits.new_empty((B * T, 2), dtype=torch.float32))
+
+
 @torch.library.custom_op("nvx::kv_compact", mutates_args=("k_cache", "v_cache"))
 def kv_compact(k_cache: Tensor, v_cache: Tensor, block_tables: Tensor, ctx_lens: Tensor,
                path: Tensor, accepted_len: Tensor) -> None:

@@ -7,7 +7,8 @@ import torch
 import nanovllm.ops  # noqa: F401
 from nanovllm.layers.attention import tree_attention
 from nanovllm.layers.sampler import (rejection_sample_tree, rejection_sample_tree_logits,
-                                     softmax_stats, temperature_softmax)
+                                     rejection_sample_tree_logits_lazy, softmax_stats,
+                                     temperature_softmax)
 from nanovllm.spec.tree import random_tree
 from nanovllm.utils.synthetic import VerifyBatch, randn_bf16
 
@@ -67,6 +68,16 @@ def test_sampler_ops(dev):
     want = rejection_sample_tree(Pf.view(B, T, V2), Q2, toks2, parents.to(torch.int32), U, Uf)
     assert all(torch.equal(a, b) for a, b in zip(got, want))
     torch.library.opcheck(torch.ops.nvx.rejection_sample_tree_logits.default, a2,
+                          test_utils=CHECKS)
+    a3 = (lg, temps, Q2, toks2, parents.to(torch.int32), U, Uf)
+    lazy = torch.ops.nvx.rejection_sample_tree_logits_lazy(*a3)
+    so = torch.full((B * T, 2), float("nan"), device=dev)
+    direct = rejection_sample_tree_logits_lazy(*a3, stats_out=so)
+    assert all(torch.equal(a, b) for a, b in zip(lazy[:4], direct[:4]))
+    assert torch.equal(torch.isnan(lazy[4]), torch.isnan(so))
+    vis = ~torch.isnan(so[:, 0])
+    assert torch.equal(lazy[4][vis], so[vis])
+    torch.library.opcheck(torch.ops.nvx.rejection_sample_tree_logits_lazy.default, a3,
                           test_utils=CHECKS)
 
 

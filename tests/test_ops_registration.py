@@ -10,14 +10,16 @@ def test_schemas_declare_the_mutated_caches():
     schemas = {n: str(getattr(torch.ops.nvx, n).default._schema)
                for n in ("store_kvcache", "kv_compact", "tree_attention", "temperature_softmax",
                          "topk_logprobs", "rejection_sample_tree", "ngram_propose",
-                         "softmax_stats", "softmax_from_stats", "rejection_sample_tree_logits")}
+                         "softmax_stats", "softmax_from_stats", "rejection_sample_tree_logits",
+                         "rejection_sample_tree_logits_lazy")}
     import re
     for n in ("store_kvcache", "kv_compact"):
         assert re.search(r"Tensor\(\w+!\) k_cache", schemas[n]), schemas[n]
         assert re.search(r"Tensor\(\w+!\) v_cache", schemas[n]), schemas[n]
         assert schemas[n].count("!") == 2, schemas[n]
     for n in ("tree_attention", "temperature_softmax", "topk_logprobs", "rejection_sample_tree",
-              "ngram_propose", "softmax_stats", "softmax_from_stats", "rejection_sample_tree_logits"):
+              "ngram_propose", "softmax_stats", "softmax_from_stats", "rejection_sample_tree_logits",
+              "rejection_sample_tree_logits_lazy"):
         assert "!" not in schemas[n], schemas[n]
     assert "Tensor? tree_mask=None" in schemas["tree_attention"]
     assert "-> (Tensor, Tensor, Tensor, Tensor)" in schemas["rejection_sample_tree"]
@@ -51,6 +53,11 @@ def test_fake_shapes_at_the_verify_step():
             logits, temps, stats, P.view(B, T, V), i32(B, T), i32(B, T),
             torch.empty(B, T, device=dev), torch.empty(B, device=dev))
         assert [o_.shape for o_ in outs] == [(B, T), (B,), (B, T), (B,)]
+        outs = torch.ops.nvx.rejection_sample_tree_logits_lazy(
+            logits, temps, P.view(B, T, V), i32(B, T), i32(B, T),
+            torch.empty(B, T, device=dev), torch.empty(B, device=dev))
+        assert [o_.shape for o_ in outs] == [(B, T), (B,), (B, T), (B,), (B * T, 2)]
+        assert outs[4].dtype == torch.float32
         lp, tok = torch.ops.nvx.topk_logprobs(logits[:2048], 8)
         assert lp.shape == tok.shape == (2048, 8) and tok.dtype == torch.int64
         d, n = torch.ops.nvx.ngram_propose(i32(4000), torch.empty(B + 1, dtype=torch.int64,
