@@ -674,6 +674,7 @@ def run_kernels(args):
     # -- causal paged prefill (the attention kernel with no tree mask), Qwen3-8B heads:
     #    4 prompts of 2048 tokens whose K/V are already in the cache
     log("tree attention (causal prefill, 8B heads)")
+    t = lambda a, dt=torch.int32: torch.from_numpy(a).to(dev, dt)  # noqa: E731
     B, Tq, Hq, Hkv, D = 4, 2048, 32, 8, 128
     rng = np.random.default_rng(args.seed + 5)
     vb = VerifyBatch([0] * B, [chain_parents(Tq)] * B, 256, rng)
