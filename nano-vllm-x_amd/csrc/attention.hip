@@ -184,6 +184,11 @@ void tree_attn_kernel(AttnParams p) {
     }
   }
   const bool use_tree = p.tree_mask != nullptr;
+  // First key that some row of this wave cannot see: the tree start with a tree mask;
+  // causal, one past the key of the wave's first node (every row of the wave sees the
+  // keys before it).  Chunks wholly before it need no mask -- in causal prefill
+  // (base 0) only the chunks on the diagonal of the wave's rows do.
+  const int mask_from = use_tree ? base : base + (row0 + wave * 32) / p.G + 1;
   const uint64_t mbits = (use_tree && row_ok && token < p.total_q) ? p.tree_mask[token] : 0ull;
 
   // Keys beyond the last node of this chunk's rows are masked for every row.
@@ -382,7 +387,7 @@ void tree_attn_kernel(AttnParams p) {
     };
     auto phase_softmax = [&]() {
       const int pos0 = c * kKC;
-      if (pos0 + kKC > base) {  // tree keys or keys past context_len
+      if (pos0 + kKC > mask_from) {  // keys some row of the wave cannot see
         // Visibility of the chunk's 64 keys for this row as one 64-bit word, cut at
         // context_len.  Tree: keys before the tree, then the row's mask bits (a tree
         // has at most 64 nodes).  Causal: keys up to base + node.  Element j of tile

@@ -5,8 +5,10 @@ The kernel (nano-vllm-x_amd/csrc/attention.hip, tree_attn_kernel, the phase_soft
 step) masks a 64-key chunk at positions pos0 .. pos0+63 with one 64-bit word per q
 row, built from the row's tree-mask bits, the tree start base = context_len - q_len
 and context_len; lane half g of a wave tests bit kt*32 + (j/4)*8 + 4g + j%4 for score
-j of S tile kt.  Chunks wholly before the tree are not masked, and a q-row chunk
-streams keys only up to key_end = min(context_len, base + last node of its rows + 1).
+j of S tile kt.  A chunk is masked only if it reaches the first key some row of the
+wave cannot see (the tree start with a tree mask; causal, one past the key of the
+wave's first node), and a q-row chunk streams keys only up to key_end =
+min(context_len, base + last node of its rows + 1).
 This restates that logic on the host, bit for bit, and compares every key of every
 chunk and row with oracle.attention.tree_visible (reference semantics: the
 bottom-right causal decode of nanovllm/layers/attention.py:72-74 generalised to a
@@ -48,7 +50,8 @@ def kernel_word(mbits, node, base, ctxlen, pos0, use_tree):
     return vis & low_bits64(ctxlen - pos0)
 
 
-def kernel_chunk_visibility(mbits, node, last_node, base, ctxlen, pos0, use_tree):
+def kernel_chunk_visibility(mbits, node, wave_first_node, last_node, base, ctxlen, pos0,
+                            use_tree):
     """Boolean [64] visibility of keys pos0 .. pos0+63 for one row as the kernel applies
     it: through the lane-half / tile / element mapping of the S accumulators, with
     keys past key_end never streamed."""
@@ -56,7 +59,8 @@ def kernel_chunk_visibility(mbits, node, last_node, base, ctxlen, pos0, use_tree
     out = np.zeros(KC, dtype=bool)
     if pos0 >= key_end:  # the chunk is not streamed at all
         return out
-    if pos0 + KC > base:
+    mask_from = base if use_tree else base + wave_first_node + 1
+    if pos0 + KC > mask_from:
         word = kernel_word(mbits, node, base, ctxlen, pos0, use_tree)
     else:
         word = ALL
@@ -73,24 +77,30 @@ def kernel_chunk_visibility(mbits, node, last_node, base, ctxlen, pos0, use_tree
     return out
 
 
-def check_sequence(parents, ctx, rows_per_chunk_nodes, use_tree):
+def check_sequence(parents, ctx, G, W, use_tree):
     """Every row and every chunk of one sequence: tree of `parents` after ctx cached
-    tokens.  rows_per_chunk_nodes: nodes per q-row chunk (W*32 rows / G heads), which
-    sets each row's last_node."""
+    tokens, G query heads per KV head (row r is node r // G), W waves of 32 rows per
+    q-row chunk (which set each row's wave and its chunk's last node)."""
     q_len = len(parents)
     ctxlen = ctx + q_len
     base = ctx
     masks = ancestor_masks(parents).view(np.uint64) if use_tree else None
     vis = tree_visible(q_len, ctxlen, masks)  # oracle, [q_len, ctxlen]
     nchunks = (ctxlen + KC - 1) // KC
-    cases = 0
-    for node in range(q_len):
-        first = (node // rows_per_chunk_nodes) * rows_per_chunk_nodes
-        last_node = min(q_len - 1, first + rows_per_chunk_nodes - 1)
+    seen, cases = set(), 0
+    for r in range(G * q_len):
+        node = r // G
+        row0 = (r // (W * 32)) * W * 32
+        wave_first_node = (row0 + ((r - row0) // 32) * 32) // G
+        last_node = min(q_len - 1, (row0 + W * 32 - 1) // G)
+        if (node, wave_first_node, last_node) in seen:
+            continue
+        seen.add((node, wave_first_node, last_node))
         mb = int(masks[node]) if use_tree else 0
         for c in range(nchunks):
             pos0 = c * KC
-            got = kernel_chunk_visibility(mb, node, last_node, base, ctxlen, pos0, use_tree)
+            got = kernel_chunk_visibility(mb, node, wave_first_node, last_node, base, ctxlen,
+                                          pos0, use_tree)
             want = np.zeros(KC, dtype=bool)
             hi = min(ctxlen, pos0 + KC)
             want[:hi - pos0] = vis[node, pos0:hi]
@@ -110,23 +120,23 @@ def test_word_matches_oracle_random_trees():
         depth = int(rng.integers(1, min(T - 1, 10) + 1)) if T > 1 else 0
         parents = random_tree(T, depth, rng) if T > 1 else np.array([-1], np.int32)
         ctx = int(rng.integers(0, 300))
-        G = int(rng.choice([1, 2, 4, 8]))
+        G = int(rng.choice([1, 2, 4, 5, 8]))
         W = int(rng.choice([4, 8]))
-        nodes_per_chunk = max(1, (W * 32) // G)
-        cases += check_sequence(parents, ctx, nodes_per_chunk, True)
+        cases += check_sequence(parents, ctx, G, W, True)
     assert cases > 50000
 
 
 def test_word_matches_oracle_causal():
     """No tree mask (decode and paged prefill): key base+m visible to row i iff m <= i,
-    for q_len 1-300 over 0-300 cached tokens, several q-row chunks per sequence."""
+    for q_len 1-300 over 0-300 cached tokens (prefill with no cached tokens included),
+    several q-row chunks per sequence; only chunks that reach past the keys every row
+    of the wave sees are masked."""
     rng = np.random.default_rng(12)
-    for _ in range(150):
+    for i in range(150):
         T = int(rng.integers(1, 301))
-        ctx = int(rng.integers(0, 300))
-        G = int(rng.choice([1, 2, 4]))
-        nodes_per_chunk = max(1, (int(rng.choice([4, 8])) * 32) // G)
-        check_sequence(chain_parents(T), ctx, nodes_per_chunk, False)
+        ctx = 0 if i % 3 == 0 else int(rng.integers(0, 300))
+        G = int(rng.choice([1, 2, 4, 5]))
+        check_sequence(chain_parents(T), ctx, G, int(rng.choice([4, 8])), False)
 
 
 def test_word_edge_offsets():
@@ -135,7 +145,7 @@ def test_word_edge_offsets():
     parents = random_tree(64, 8, np.random.default_rng(3))
     masks = ancestor_masks(parents).view(np.uint64)
     for ctx in list(range(0, 130)) + [191, 192, 193, 255, 256, 257]:
-        check_sequence(parents, ctx, 64, True)
+        check_sequence(parents, ctx, 4, 8, True)
     assert int(masks[63]) >> 63 == 1
 
 
