@@ -19,8 +19,9 @@
 //
 // Pipeline: a 2-stage LDS ring (64 KB), one chunk in flight while the other is
 // computed, one barrier per chunk.  Waves use < 256 registers, so a CU runs two per
-// SIMD: a work item of more than 128 rows is one 8-wave workgroup (its K/V enters
-// the CU once), smaller items are 4-wave workgroups, two per CU.  The two waves on
+// SIMD: a tree-sized work item of more than 128 rows is one 8-wave workgroup (its K/V
+// enters the CU once); smaller items and the q-row chunks of causal prefill are
+// 4-wave workgroups, two per CU.  The two waves on
 // a SIMD interleave their MFMA and VALU phases.
 //
 // Masking: keys < context_len - q_len are visible to all rows; key base+m is
@@ -561,14 +562,18 @@ struct Plan {
   int nq, nsplit, waves;
 };
 
-// Waves per workgroup.  A work item of more than 128 q rows (a GQA group of four
-// heads over a 64-node tree: 256 rows) gets one 8-wave workgroup, so its K/V is
-// streamed into one CU once; the alternative, two 4-wave workgroups per item
-// meeting in L2, streams it twice through the CUs' load path.  Measured at 64
-// sequences of 64-node trees over 2k keys (32/8 heads), each launch after a
-// 4096 x 4096 x 6144 GEMM: 150-153 us against 160-164 us.  One 8-wave
-// workgroup fills a CU (two waves per SIMD).
-int waves_for(int rows) { return rows > 128 ? 8 : 4; }
+// Waves per workgroup.  A tree-sized work item (at most 64 q rows per sequence) of
+// more than 128 q rows (a GQA group of four heads over a 64-node tree: 256 rows) gets
+// one 8-wave workgroup, so its K/V is streamed into one CU once; the alternative,
+// two 4-wave workgroups per item meeting in L2, streams it twice through the CUs'
+// load path.  Measured at 64 sequences of 64-node trees over 2k keys (32/8 heads),
+// each launch after a 4096 x 4096 x 6144 GEMM: 150-153 us against 160-164 us.  One
+// 8-wave workgroup fills a CU (two waves per SIMD).  Longer q (causal prefill) splits
+// into many q-row chunks that re-read the same K/V through L2 anyway; there 4-wave
+// workgroups, two per CU, let one workgroup's start (Q and first-chunk loads) and end
+// overlap the other's chunks: 4 prompts of 2048 tokens at 32/8 heads 155 us against
+// 159 us, 16 prompts of 1024 tokens at 16/8 heads 105 us against 115 us.
+int waves_for(int rows, int max_q) { return rows > 128 && max_q <= 64 ? 8 : 4; }
 
 // Chunks one KV split may span: its pages (at most ceil(span / block_size) + 1 of
 // them) must fit the workgroup's LDS page table.
@@ -582,7 +587,7 @@ Plan make_plan(int num_seqs, int max_q, int max_ctx, int Hq, int Hkv, int block_
   const int G = Hq / Hkv;
   const int rows = G * (max_q > 0 ? max_q : 1);
   Plan pl;
-  pl.waves = waves_for(rows);
+  pl.waves = waves_for(rows, max_q);
   pl.nq = (rows + pl.waves * 32 - 1) / (pl.waves * 32);
   const int64_t waves = (int64_t)num_seqs * Hkv * pl.nq * pl.waves;
   int ns = (int)((kTargetWaves + waves - 1) / (waves > 0 ? waves : 1));
