@@ -25,6 +25,12 @@ speculation (`--spec none`); value = output tokens/s.
 sampler, n-gram drafter, tree attention at the Qwen3-0.6B shape, and the KV
 scatter, compaction, softmax, tree rejection walk and draft top-k at the verify-step
 shape) against the oracle on the host, one JSON line per workload.
+
+`--workload power` runs loads back to back for a few seconds each while sampling the
+socket power (`amd-smi metric -p`) and shader clock (`rocm-smi --showclocks`): idle,
+tree attention at the verify-step layer shape and in causal prefill, a bf16 GEMM and a
+device copy.  From the GEMM (energy per MFMA FLOP) and the copy (energy per HBM byte)
+it derives the shortest time the power cap allows for the verify-step attention layer.
 """
 import argparse
 import json
@@ -63,7 +69,9 @@ def parse():
                          "trees, ctx 1024-4096) with a parity check on 2 sequences")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device copy (HBM counter calibration)")
-    ap.add_argument("--workload", choices=("verify", "e2e", "kernels"), default="verify")
+    ap.add_argument("--workload", choices=("verify", "e2e", "kernels", "power"), default="verify")
+    ap.add_argument("--power-secs", type=float, default=4.0,
+                    help="seconds of back-to-back launches per load in --workload power")
     ap.add_argument("--spec", choices=("eagle3", "ngram", "none"), default="eagle3",
                     help="e2e: speculative method")
     ap.add_argument("--e2e-seqs", type=int, default=256)
@@ -836,6 +844,199 @@ def run_kernels(args):
          f"{ns} of {rows} rows, scaled", ok)
 
 
+def smi_reading():
+    """One reading of the socket power (W, `amd-smi metric -p`) and the shader clock (MHz,
+    `rocm-smi --showclocks`); None for a value the tools do not report."""
+    import re
+    import subprocess
+    power = sclk = None
+    try:
+        r = subprocess.run(["amd-smi", "metric", "-p", "--json"], capture_output=True, text=True,
+                           timeout=10)
+        m = re.search(r'"socket_power"\s*:\s*\{[^}]*"value"\s*:\s*([0-9.]+)', r.stdout)
+        power = float(m.group(1)) if m else None
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        r = subprocess.run(["rocm-smi", "--showclocks", "--json"], capture_output=True, text=True,
+                           timeout=10)
+        m = re.search(r'"sclk clock speed:"\s*:\s*"\((\d+)Mhz\)"', r.stdout)
+        sclk = float(m.group(1)) if m else None
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return power, sclk
+
+
+def power_cap_w():
+    """The board's power cap (W) from `rocm-smi --showmaxpower`, or None."""
+    import re
+    import subprocess
+    try:
+        r = subprocess.run(["rocm-smi", "--showmaxpower", "--json"], capture_output=True, text=True,
+                           timeout=10)
+    except (OSError, subprocess.SubprocessError):
+        return None
+    m = re.search(r'"Max Graphics Package Power \(W\)"\s*:\s*"([0-9.]+)"', r.stdout)
+    return float(m.group(1)) if m else None
+
+
+def powered_run(torch, fn, secs, batch=20):
+    """Call fn back to back for about secs seconds (synchronising every `batch` calls)
+    while a thread samples power and clock every ~0.2 s.  Returns (GPU µs per call from
+    CUDA events, power readings, clock readings); the first two readings, taken while
+    the part ramps up, are dropped."""
+    import threading
+    samples, stop = [], threading.Event()
+
+    def poll():
+        while not stop.is_set():
+            samples.append(smi_reading())
+            time.sleep(0.2)
+
+    for _ in range(batch):
+        fn()
+    torch.cuda.synchronize()
+    th = threading.Thread(target=poll)
+    calls = 0
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    th.start()
+    e0.record()
+    t0 = time.time()
+    while time.time() - t0 < secs:
+        for _ in range(batch):
+            fn()
+        calls += batch
+        torch.cuda.synchronize()
+    e1.record()
+    torch.cuda.synchronize()
+    stop.set()
+    th.join()
+    body = samples[2:] if len(samples) > 4 else samples
+    return (e0.elapsed_time(e1) * 1e3 / calls, [p for p, _ in body if p is not None],
+            [c for _, c in body if c is not None])
+
+
+def run_power(args):
+    """Power and clock under the verify-step attention layer, causal prefill, a bf16 GEMM
+    and a device copy, each run back to back for --power-secs seconds; one JSON line per
+    load and one with the energy budget of the attention layer at the power cap.
+
+    The budget: at the cap, a launch of t us may spend (cap - idle) * t above idle, so
+    0.60 of the 8 TB/s roofline (t = algorithmic bytes / 4.8 TB/s) allows that much
+    energy per launch.  Against it stand the energy the layer spends now, (measured
+    power - idle) * measured time, and its HBM share at the copy's energy per byte; the
+    rest, per MFMA FLOP executed, is compared with the GEMM's energy per FLOP (which
+    includes the GEMM's own LDS and VALU work)."""
+    import threading
+    import numpy as np
+    import torch
+    from nanovllm import _C
+    from nanovllm.layers.attention import tree_attention
+    from nanovllm.spec.tree import chain_parents, random_tree
+    from nanovllm.utils.synthetic import VerifyBatch
+
+    _C.lib()
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    D = 128
+
+    def stat(a):
+        return {"mean": float(np.mean(a)), "min": float(np.min(a)), "max": float(np.max(a)),
+                "n": len(a)} if a else None
+
+    def attention_load(vb, Hq, Hkv, T, masked):
+        kc = torch.randn(vb.num_blocks, 256, Hkv, D, device=dev, generator=g).to(torch.bfloat16)
+        vc = torch.randn(vb.num_blocks, 256, Hkv, D, device=dev, generator=g).to(torch.bfloat16)
+        N = int(vb.cu_q[-1])
+        q = torch.randn(N, Hq, D, device=dev, generator=g).to(torch.bfloat16)
+        t = lambda a, dt=torch.int32: torch.from_numpy(np.ascontiguousarray(a)).to(dev, dt)  # noqa: E731
+        a_args = (q, kc, vc, t(vb.bt), t(vb.cu_q), t(vb.context_lens), D ** -0.5,
+                  t(vb.masks, torch.int64) if masked else None, T, int(vb.context_lens.max()))
+        out = torch.empty_like(q)
+        if masked:  # MFMA FLOPs executed: every q row against every key of its 64-key chunks
+            chunks = np.ceil(vb.context_lens / 64.0) * 64.0
+            flops = 4.0 * Hq * D * float((vb.qlens * chunks).sum())
+        else:  # causal: the FLOPs of the visible keys
+            ql, cl = vb.qlens.astype(np.float64), vb.context_lens.astype(np.float64)
+            flops = 4.0 * Hq * D * float(((cl - ql) * ql + ql * (ql + 1) / 2).sum())
+        nbytes = float(vb.context_lens.sum()) * Hkv * D * 2 * 2 + 2.0 * N * Hq * D * 2
+        return (lambda: tree_attention(*a_args, out=out)), flops, nbytes
+
+    cap = power_cap_w()
+    # idle: no launches
+    samples, stop = [], threading.Event()
+
+    def poll():
+        while not stop.is_set():
+            samples.append(smi_reading())
+            time.sleep(0.2)
+
+    th = threading.Thread(target=poll)
+    th.start()
+    time.sleep(2.0)
+    stop.set()
+    th.join()
+    idle_w = [p for p, _ in samples if p is not None]
+    idle = float(np.mean(idle_w)) if idle_w else None
+    print(json.dumps({"workload": "power", "load": "idle", "power_w": stat(idle_w),
+                      "sclk_mhz": stat([c for _, c in samples if c is not None]),
+                      "power_cap_w": cap}), flush=True)
+
+    rng = np.random.default_rng(args.seed)
+    B, T = 64, 64
+    vb4 = VerifyBatch([2048] * B, [random_tree(T, 8, rng) for _ in range(B)], 256, rng)
+    vbp = VerifyBatch([0] * 4, [chain_parents(2048)] * 4, 256, rng)
+    M = 8192
+    A = torch.randn(M, M, device=dev, generator=g).to(torch.bfloat16)
+    Bm = torch.randn(M, M, device=dev, generator=g).to(torch.bfloat16)
+    C = torch.empty(M, M, device=dev, dtype=torch.bfloat16)
+    src = torch.randint(0, 255, (1 << 30,), device=dev, dtype=torch.uint8, generator=g)
+    dst = torch.empty_like(src)
+    att4, f4, b4 = attention_load(vb4, 32, 8, T, True)
+    attp, fp, bp = attention_load(vbp, 32, 8, 2048, False)
+    loads = [
+        ("tree attention, verify-step layer: 64 sequences x 64-node depth-8 trees, ctx 2048, "
+         "32/8 heads", att4, f4, b4),
+        ("tree attention, causal prefill: 4 prompts of 2048 tokens, 32/8 heads", attp, fp, bp),
+        ("bf16 GEMM 8192 x 8192 x 8192 (torch.mm)", lambda: torch.mm(A, Bm, out=C),
+         2.0 * M * M * M, 3.0 * M * M * 2),
+        ("device copy, 1 GiB (read + write)", lambda: dst.copy_(src), 0.0, 2.0 * src.numel()),
+    ]
+    res = {}
+    for name, fn, flops, nbytes in loads:
+        us, pw, ck = powered_run(torch, fn, args.power_secs)
+        p = float(np.mean(pw)) if pw else None
+        above = (p - idle) * us * 1e-3 if (p is not None and idle is not None) else None  # mJ
+        rec = {"workload": "power", "load": name, "us_per_call": us, "power_w": stat(pw),
+               "sclk_mhz": stat(ck), "mj_per_call_above_idle": above,
+               "tflops": flops / us / 1e6 if flops else None, "gbs": nbytes / us / 1e3}
+        res[name] = (us, p, flops, nbytes)
+        print(json.dumps(rec), flush=True)
+
+    gemm = res[loads[2][0]]
+    copy = res[loads[3][0]]
+    if None in (idle, cap, gemm[1], copy[1]):
+        print(json.dumps({"workload": "power", "floor": None,
+                          "note": "power readings unavailable"}), flush=True)
+        return
+    layer = res[loads[0][0]]
+    e_flop = (gemm[1] - idle) * gemm[0] * 1e-6 / gemm[2]  # J per FLOP above idle
+    e_byte = (copy[1] - idle) * copy[0] * 1e-6 / copy[3]  # J per HBM byte above idle
+    e_now = (layer[1] - idle) * layer[0] * 1e-6  # J per launch above idle
+    t_target = b4 / (0.60 * HBM_PEAK_GBS * 1e9)  # s
+    e_budget = (cap - idle) * t_target
+    e_hbm = b4 * e_byte
+    print(json.dumps({"workload": "power", "budget": "verify-step attention layer at the cap",
+                      "measured_us": layer[0], "measured_power_w": layer[1],
+                      "mj_per_launch_now": e_now * 1e3, "target_frac_of_hbm_peak": 0.60,
+                      "target_us": t_target * 1e6, "mj_per_launch_allowed_at_cap": e_budget * 1e3,
+                      "hbm_mj_at_copy_energy": e_hbm * 1e3, "layer_mfma_flops": f4,
+                      "pj_per_flop_rest_now": (e_now - e_hbm) / f4 * 1e12,
+                      "pj_per_flop_rest_allowed": (e_budget - e_hbm) / f4 * 1e12,
+                      "pj_per_flop_gemm": e_flop * 1e12, "pj_per_byte_copy": e_byte * 1e12}),
+          flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -847,6 +1048,9 @@ def main():
         return
     if args.workload == "kernels":
         run_kernels(args)
+        return
+    if args.workload == "power":
+        run_power(args)
         return
     import torch
     from nanovllm import _C
