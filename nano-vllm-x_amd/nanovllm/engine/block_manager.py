@@ -20,6 +20,11 @@ Keys chain block by block: key(i) = xxh3_64(int32 tokens of block i, seed=key(i-
 seed 0 for block 0, so equal keys name equal prefixes.  A sequence caches the keys
 of its full blocks (``Sequence.block_hashes``); its history only grows, so they stay
 valid across steps and preemptions.
+
+With ``key_next_token`` (EAGLE-3 drafting) a block's key and content also cover the
+token after the block: the draft K/V row at position p is computed from token p+1,
+so the block's last draft row belongs to the prefix only together with that token.
+A block is then published once that token is in the history.
 """
 from collections import OrderedDict
 
@@ -37,10 +42,11 @@ def block_key(token_ids, parent_key: int = 0) -> int:
 
 class BlockManager:
 
-    def __init__(self, num_blocks: int, block_size: int):
+    def __init__(self, num_blocks: int, block_size: int, key_next_token: bool = False):
         if num_blocks <= 0 or block_size <= 0:
             raise ValueError("BlockManager: num_blocks and block_size must be positive")
         self.block_size = block_size
+        self.key_next_token = key_next_token
         self.num_blocks = num_blocks
         self.refs = np.zeros(num_blocks, dtype=np.int32)
         self.keys: list[int | None] = [None] * num_blocks
@@ -77,10 +83,27 @@ class BlockManager:
             self.free[block_id] = None
 
     # ---------------------------------------------------------- prefix cache
+    def _content(self, seq: Sequence, i: int) -> list[int]:
+        """What block i's key covers: its tokens, and with key_next_token the token after
+        it (which the caller guarantees is in the history)."""
+        toks = seq.block(i)
+        if self.key_next_token:
+            toks = toks + [seq.token_ids[(i + 1) * self.block_size]]
+        return toks
+
+    def _keyable(self, seq: Sequence) -> int:
+        """Number of leading blocks whose key the history determines."""
+        if self.key_next_token:
+            return (len(seq) - 1) // self.block_size
+        return len(seq) // self.block_size
+
     def _keys_of(self, seq: Sequence, num_full_blocks: int) -> list[int]:
         keys = seq.block_hashes
+        if num_full_blocks > self._keyable(seq):
+            raise ValueError(f"sequence {seq.seq_id}: the keys of {num_full_blocks} blocks need "
+                             f"tokens past its {len(seq)}")
         for i in range(len(keys), num_full_blocks):
-            keys.append(block_key(seq.block(i), keys[i - 1] if i else 0))
+            keys.append(block_key(self._content(seq, i), keys[i - 1] if i else 0))
         return keys
 
     def _cached_prefix(self, seq: Sequence) -> list[int]:
@@ -91,7 +114,7 @@ class BlockManager:
         hits = []
         for i, key in enumerate(self._keys_of(seq, candidates)[:candidates]):
             b = self.index.get(key)
-            if b is None or self.contents[b] != tuple(seq.block(i)):
+            if b is None or self.contents[b] != tuple(self._content(seq, i)):
                 break
             hits.append(b)
         return hits
@@ -146,12 +169,12 @@ class BlockManager:
         if num_cached_tokens is None:
             num_cached_tokens = seq.num_cached_tokens + seq.num_scheduled_tokens
         first = seq.num_cached_tokens // self.block_size
-        last = num_cached_tokens // self.block_size
+        last = min(num_cached_tokens // self.block_size, self._keyable(seq))
         if last <= first:
             return
         keys = self._keys_of(seq, last)
         for i in range(first, last):
             b = seq.block_table[i]
             self.keys[b] = keys[i]
-            self.contents[b] = tuple(seq.block(i))
+            self.contents[b] = tuple(self._content(seq, i))
             self.index[keys[i]] = b

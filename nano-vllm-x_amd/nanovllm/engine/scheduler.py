@@ -35,7 +35,10 @@ class Scheduler:
         self.eos = config.eos
         self.block_size = config.kvcache_block_size
         self.lookahead = config.verify_lookahead
-        self.block_manager = BlockManager(config.num_kvcache_blocks, config.kvcache_block_size)
+        # EAGLE-3's draft K/V row at position p depends on token p+1: prefix-cache keys
+        # then cover the token after each block
+        self.block_manager = BlockManager(config.num_kvcache_blocks, config.kvcache_block_size,
+                                          key_next_token=config.speculative_method == "eagle3")
         self.waiting: deque[Sequence] = deque()
         self.running: deque[Sequence] = deque()
 
@@ -115,15 +118,20 @@ class Scheduler:
                                    f"one token id >= 0 (got {new})")
             if is_prefill:
                 cached = seq.num_cached_tokens + seq.num_scheduled_tokens
-                bm.hash_blocks(seq, cached)
-                seq.num_cached_tokens = cached
                 seq.num_scheduled_tokens = 0
-                if cached < len(seq):
-                    continue  # a prompt chunk: no token is sampled yet
+                if cached < len(seq):  # a prompt chunk: no token is sampled yet
+                    bm.hash_blocks(seq, cached)
+                    seq.num_cached_tokens = cached
+                    continue
             else:
                 seq.num_verify_steps += 1
                 seq.num_accepted_draft += len(new) - 1
             seq.extend_until_stop(new, self.eos)
+            if is_prefill:
+                # published after the sampled token joins the history, so a block that
+                # ends the prompt can carry the token after it in its key
+                bm.hash_blocks(seq, cached)
+                seq.num_cached_tokens = cached
             if seq.is_finished:
                 bm.deallocate(seq)
                 self.running.remove(seq)

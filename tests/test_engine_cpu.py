@@ -154,6 +154,55 @@ def test_prefix_cache_reuse_release_and_eviction():
         bm.allocate(c, 0)                    # c already holds blocks
 
 
+def test_draft_prefix_keys_cover_the_next_token():
+    """EAGLE-3 drafting (key_next_token): the draft K/V row at a block's last position is
+    computed from the token after the block, so a prefix hit needs that token to match
+    too.  Two prompts sharing a full block but differing in the next token share nothing;
+    with the same next token they share the block.  Without the flag the next token
+    plays no part."""
+    for flag, hits_diff in ((True, 0), (False, 1)):
+        bm = BlockManager(8, BS, key_next_token=flag)
+        a = Sequence(list(range(300)))
+        bm.allocate(a, bm.can_allocate(a))
+        a.num_scheduled_tokens = 300
+        bm.hash_blocks(a)
+        a.num_cached_tokens, a.num_scheduled_tokens = 300, 0
+        diff = Sequence(list(range(256)) + [9999] + list(range(257, 300)))
+        same = Sequence(list(range(290)))
+        assert bm.can_allocate(diff) == hits_diff
+        assert bm.can_allocate(same) == 1
+    # a block's key is never formed before the token after it exists
+    bm = BlockManager(8, BS, key_next_token=True)
+    full = Sequence(list(range(2 * BS)))
+    bm.allocate(full, 0)
+    full.num_scheduled_tokens = 2 * BS
+    bm.hash_blocks(full)                      # block 1's next token is not known yet
+    assert len(full.block_hashes) == 1 and bm.keys[full.block_table[1]] is None
+    with pytest.raises(ValueError):
+        bm._keys_of(full, 2)
+
+
+def test_eagle_prefill_publishes_the_prompt_end_block_after_sampling():
+    """With EAGLE-3 the scheduler publishes a prefill's blocks after the sampled token
+    joins the history, so a prompt that ends on a block boundary still publishes its
+    last block (keyed with the sampled token)."""
+    cfg = Config("unused", hf_config=Qwen3Config(max_position_embeddings=8192),
+                 num_kvcache_blocks=16, speculative_method="eagle3", num_speculative_tokens=31)
+    cfg.eos = EOS
+    Sequence.block_size = BS
+    s = Scheduler(cfg)
+    assert s.block_manager.key_next_token
+    a = Sequence(prompt(2 * BS), SamplingParams(max_tokens=8))
+    s.add(a)
+    run_prefill(s)                            # samples token 11 after the prompt
+    bm = s.block_manager
+    assert a.num_cached_tokens == 2 * BS and a.token_ids[-1] == 11
+    assert all(bm.keys[b] is not None for b in a.block_table[:2])
+    # a later prompt continuing with the same token hits both blocks, another does not
+    assert bm.can_allocate(Sequence(prompt(2 * BS) + [11, 12])) == 2
+    assert bm.can_allocate(Sequence(prompt(2 * BS) + [13, 12])) == 1
+
+
 def test_chunked_prefill_fills_the_budget():
     """The token budget is filled: the last sequence admitted may take a chunk and
     stays at the head of the waiting queue until its prompt is cached."""

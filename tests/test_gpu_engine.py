@@ -243,6 +243,30 @@ def test_eagle3_deep_acceptance_is_lossless(dev):
 
 
 @pytest.mark.gpu
+def test_eagle3_prefix_hits_need_the_next_token(dev):
+    """EAGLE-3 with the prefix cache: the draft K/V row at a block's last position comes
+    from the token after the block, so a prompt that shares a full block with a finished
+    one but continues with another token must not hit it, and one that continues with
+    the same token does.  Both generate the target's greedy output."""
+    V = 64
+    llm = LLM("unused", hf_config=tiny_config(vocab=V, layers=4), num_kvcache_blocks=64,
+              speculative_method="eagle3", num_speculative_tokens=15, eagle_topk=8, eagle_depth=4,
+              max_num_batched_tokens=4096, enforce_eager=True)
+    rng = np.random.default_rng(11)
+    base = rng.integers(0, V, size=300).tolist()
+    other = list(base)
+    other[256] = (base[256] + 1) % V
+    sp = SamplingParams(temperature=0.0, max_tokens=24, ignore_eos=True)
+    outs = llm.generate([base], sp, use_tqdm=False)
+    bm = llm.scheduler.block_manager
+    assert bm.can_allocate(Sequence(other)) == 0
+    assert bm.can_allocate(Sequence(base[:280])) == 1
+    ps = [other, base[:280]]
+    outs = llm.generate(ps, sp, use_tqdm=False)
+    check_greedy_is_argmax(llm, ps, outs, 24)
+
+
+@pytest.mark.gpu
 def test_eagle3_sampling_runs(dev):
     V = 64
     llm = LLM("unused", hf_config=tiny_config(vocab=V, layers=6), num_kvcache_blocks=64,
