@@ -1106,6 +1106,10 @@ def main():
     walk_ms = avg("rejection")
     sampler_bytes = stats_bytes + walk_bytes
     sampler_gbs = sampler_bytes / (walk_ms * 1e-3) / 1e9
+    # The dense form of the sampler reads every fp32 target and draft probability row
+    # ([B, T, V] each); its HBM roofline time is what the walk is measured against.
+    dense_bytes = 2.0 * B * T * V * 4
+    dense_us = dense_bytes / (HBM_PEAK_GBS * 1e9) * 1e6
 
     out = {
         "metric": METRIC,
@@ -1141,7 +1145,10 @@ def main():
                     "residual_bytes_per_step": walk_bytes,
                     "bytes_per_step": sampler_bytes,
                     "us_per_step": walk_ms * 1e3,
-                    "GBs": sampler_gbs, "frac": sampler_gbs / HBM_PEAK_GBS},
+                    "GBs": sampler_gbs, "frac": sampler_gbs / HBM_PEAK_GBS,
+                    "dense_bytes_per_step": dense_bytes,
+                    "dense_roofline_us": dense_us,
+                    "time_vs_dense_roofline": walk_ms * 1e3 / dense_us},
         "kernels_us_per_step": {k: v[0] / args.steps * 1e3 for k, v in timers.items()},
     }
     if args.small_tree_attention:
