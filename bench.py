@@ -12,6 +12,9 @@ and tokens are synthetic (seeded).  value = verified tokens/s = sum over the tim
 steps of sum_b (accepted_len_b + 1) / elapsed.
 
 Prints one JSON line.  `--gpus N` with N > 1 exits: the verify path runs on a single GPU.
+After the verify step (outside its timed region) the line also carries the Qwen3-0.6B-shape
+tree attention (`tree_attention_0p6b`) and the offline generate workload below, run in a
+child process (`offline_generate`; `--no-offline-generate` skips it).
 
 `--workload e2e` runs the offline engine benchmark instead, with the methodology
 of the reference's bench.py (256 requests, prompt token ids uniform over the
@@ -67,6 +70,9 @@ def parse():
     ap.add_argument("--small-tree-attention", action=argparse.BooleanOptionalAction, default=True,
                     help="also time tree attention at the Qwen3-0.6B shape (batch 32, 32-node "
                          "trees, ctx 1024-4096) with a parity check on 2 sequences")
+    ap.add_argument("--offline-generate", action=argparse.BooleanOptionalAction, default=True,
+                    help="after the verify step, run the offline generate workload (--workload e2e) "
+                         "in a child process and add its summary to the JSON line")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device copy (HBM counter calibration)")
     ap.add_argument("--workload", choices=("verify", "e2e", "kernels", "power"), default="verify")
@@ -1179,7 +1185,30 @@ def main():
                       f"the full verify step on the host: torch-CPU fp32 dense layers + oracle "
                       f"tree attention, softmax, rejection sampling, compaction; {secs:.1f} s",
             **host_info(torch)}
+    if args.offline_generate:
+        print("[bench] offline generate (Qwen3-0.6B shape, EAGLE-3) in a child process",
+              file=sys.stderr, flush=True)
+        out["offline_generate"] = offline_generate_record()
     print(json.dumps(out), flush=True)
+
+
+def offline_generate_record():
+    """The offline generate workload (`--workload e2e`: the reference bench.py workload at
+    the Qwen3-0.6B shape with EAGLE-3 drafting and HIP graphs) run in a child process, with
+    its own engine and memory, summarised for the verify step's JSON line.  A failure is
+    recorded in the summary, not raised."""
+    import subprocess
+    cmd = [sys.executable, os.path.abspath(__file__), "--workload", "e2e"]
+    try:
+        r = subprocess.run(cmd, stdout=subprocess.PIPE, text=True, timeout=900)
+    except subprocess.TimeoutExpired:
+        return {"error": "timed out after 900 s"}
+    lines = [ln for ln in r.stdout.splitlines() if ln.startswith("{")]
+    if r.returncode != 0 or not lines:
+        return {"error": f"exit code {r.returncode}"}
+    d = json.loads(lines[-1])
+    return {k: d[k] for k in ("metric", "value", "unit", "elapsed_s", "output_tokens",
+                              "mean_accepted_per_verify", "config") if k in d}
 
 
 if __name__ == "__main__":
