@@ -850,40 +850,47 @@ def run_kernels(args):
          f"{ns} of {rows} rows, scaled", ok)
 
 
+def parse_socket_power(text):
+    """Socket power (W) from `amd-smi metric -p --json` output, or None."""
+    import re
+    m = re.search(r'"socket_power"\s*:\s*\{[^}]*"value"\s*:\s*([0-9.]+)', text)
+    return float(m.group(1)) if m else None
+
+
+def parse_sclk(text):
+    """Shader clock (MHz) from `rocm-smi --showclocks --json` output (which may start
+    with a warning line), or None."""
+    import re
+    m = re.search(r'"sclk clock speed:"\s*:\s*"\((\d+)Mhz\)"', text)
+    return float(m.group(1)) if m else None
+
+
+def parse_power_cap(text):
+    """Power cap (W) from `rocm-smi --showmaxpower --json` output, or None."""
+    import re
+    m = re.search(r'"Max Graphics Package Power \(W\)"\s*:\s*"([0-9.]+)"', text)
+    return float(m.group(1)) if m else None
+
+
+def tool_output(*cmd):
+    """stdout of a system tool, or "" when it is missing or fails to answer."""
+    import subprocess
+    try:
+        return subprocess.run(list(cmd), capture_output=True, text=True, timeout=10).stdout
+    except (OSError, subprocess.SubprocessError):
+        return ""
+
+
 def smi_reading():
     """One reading of the socket power (W, `amd-smi metric -p`) and the shader clock (MHz,
     `rocm-smi --showclocks`); None for a value the tools do not report."""
-    import re
-    import subprocess
-    power = sclk = None
-    try:
-        r = subprocess.run(["amd-smi", "metric", "-p", "--json"], capture_output=True, text=True,
-                           timeout=10)
-        m = re.search(r'"socket_power"\s*:\s*\{[^}]*"value"\s*:\s*([0-9.]+)', r.stdout)
-        power = float(m.group(1)) if m else None
-    except (OSError, subprocess.SubprocessError):
-        pass
-    try:
-        r = subprocess.run(["rocm-smi", "--showclocks", "--json"], capture_output=True, text=True,
-                           timeout=10)
-        m = re.search(r'"sclk clock speed:"\s*:\s*"\((\d+)Mhz\)"', r.stdout)
-        sclk = float(m.group(1)) if m else None
-    except (OSError, subprocess.SubprocessError):
-        pass
-    return power, sclk
+    return (parse_socket_power(tool_output("amd-smi", "metric", "-p", "--json")),
+            parse_sclk(tool_output("rocm-smi", "--showclocks", "--json")))
 
 
 def power_cap_w():
     """The board's power cap (W) from `rocm-smi --showmaxpower`, or None."""
-    import re
-    import subprocess
-    try:
-        r = subprocess.run(["rocm-smi", "--showmaxpower", "--json"], capture_output=True, text=True,
-                           timeout=10)
-    except (OSError, subprocess.SubprocessError):
-        return None
-    m = re.search(r'"Max Graphics Package Power \(W\)"\s*:\s*"([0-9.]+)"', r.stdout)
-    return float(m.group(1)) if m else None
+    return parse_power_cap(tool_output("rocm-smi", "--showmaxpower", "--json"))
 
 
 def powered_run(torch, fn, secs, batch=20):

@@ -96,3 +96,23 @@ def test_verify_batch_layout():
     assert vb.positions[:8].tolist() == (300 + depths(trees[0])).tolist()
     bt, n = paged_block_tables([10, 600], 256, rng)
     assert n == 4 and sorted(bt[bt >= 0].tolist()) == [0, 1, 2, 3]
+
+
+def test_power_tool_parsing():
+    """bench.py --workload power reads the socket power, shader clock and power cap from
+    the JSON that amd-smi and rocm-smi print on the MI355X box (samples captured there;
+    rocm-smi may put a warning line before its JSON)."""
+    import bench
+    amd = ('{\n    "gpu_data": [\n        {\n            "gpu": 0,\n            "power": {\n'
+           '                "socket_power": {\n                    "value": 1398,\n'
+           '                    "unit": "W"\n                },\n'
+           '                "gfx_voltage": "N/A"\n            }\n        }\n    ]\n}\n')
+    smi = ('WARNING: AMD GPU device(s) is/are in a low-power state. Check power '
+           'control/runtime_status\n\n{"card0": {"mclk clock speed:": "(2000Mhz)", '
+           '"mclk clock level:": "0", "sclk clock speed:": "(1667Mhz)", "sclk clock level:": "S", '
+           '"Max Graphics Package Power (W)": "1400.0"}}\n')
+    assert bench.parse_socket_power(amd) == 1398.0
+    assert bench.parse_sclk(smi) == 1667.0
+    assert bench.parse_power_cap(smi) == 1400.0
+    for f in (bench.parse_socket_power, bench.parse_sclk, bench.parse_power_cap):
+        assert f("") is None and f("N/A") is None
