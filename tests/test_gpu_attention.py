@@ -115,6 +115,37 @@ def test_causal_prefill_long_queries(dev):
 
 
 @pytest.mark.gpu
+def test_causal_wave_plans_agree(dev):
+    """Causal launches with at most 64 q rows per sequence and more than 128 rows per KV
+    head run 8-wave workgroups; longer q (prefill) runs 4-wave workgroups, two per CU.
+    The same prompt with q = 64 and q = 65 at 32/8 heads behind a cached prefix takes each
+    path: both match the oracle, and the 64 shared tokens' outputs agree bit for bit
+    (rows keep their 32-row waves and see the same chunks in the same order)."""
+    Hq, Hkv, D, bs = 32, 8, 128, 256
+    rng = np.random.default_rng(21)
+    g = torch.Generator().manual_seed(21)
+    vb = VerifyBatch([300, 190], [chain_parents(65), chain_parents(65)], bs, rng)
+    kc = randn_bf16((vb.num_blocks, bs, Hkv, D), g)
+    vc = randn_bf16((vb.num_blocks, bs, Hkv, D), g)
+    q = randn_bf16((int(vb.cu_q[-1]), Hq, D), g)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    outs = {}
+    for T in (65, 64):
+        # the first T tokens of each sequence: the same cache, context shortened by 65 - T
+        cu = np.array([0, T, 2 * T], dtype=np.int32)
+        cl = (vb.context_lens - (65 - T)).astype(np.int32)
+        qq = torch.cat([q[int(vb.cu_q[b]):int(vb.cu_q[b]) + T] for b in range(2)])
+        o = tree_attention(qq.to(dev), kc.to(dev), vc.to(dev), t(vb.bt), t(cu), t(cl), D ** -0.5,
+                           None)
+        ref = oatt.paged_attention(qq.float().numpy(), kc.float().numpy(), vc.float().numpy(),
+                                   vb.bt, cu, cl, None, D ** -0.5, bs)
+        assert np.abs(o.cpu().float().numpy() - ref).max() < TOL, T
+        outs[T] = o.cpu()
+    shared = torch.cat([outs[65][0:64], outs[65][65:129]])
+    assert torch.equal(shared, outs[64])
+
+
+@pytest.mark.gpu
 def test_config3_tree32_qwen3_0p6b(dev):
     """Qwen3-0.6B shape: 16 q heads, 8 KV heads, B=32, ctx U[1024,4096], 32-node
     depth-6 trees, pages scattered randomly (the split-KV path)."""
